@@ -1,0 +1,408 @@
+// backend.cpp -- the slate_backend_t vtable for gfx950 and the extension
+// entries (include/slate_hip.h).  Host code only; kernels live in k_*.hip.
+//
+// The vtable keeps the contract of include/slate/backend.h:41-99: pointers
+// passed to compute entries are device pointers from alloc(); copies are
+// synchronous with respect to the host buffers; sync() waits for all work.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "launch.h"
+
+namespace slate_hip {
+
+// ---------------------------------------------------------------------------
+static std::mutex g_err_mu;
+static std::string g_err;
+static int g_err_code = 0;
+
+void set_error(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    if (g_err_code == 0) {           // keep the first error until cleared
+        g_err_code = code ? code : -7;
+        g_err = buf;
+    }
+    if (getenv("SLATE_HIP_VERBOSE")) fprintf(stderr, "slate_hip: %s\n", buf);
+}
+
+int error_code() {
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    return g_err_code;
+}
+
+// ---------------------------------------------------------------------------
+static std::once_flag g_init_once;
+static int g_device = -1;
+static hipStream_t g_stream = nullptr;
+static bool g_ok = false;
+
+static void init_device() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        set_error(-7, "no HIP device available");
+        return;
+    }
+    for (int d = 0; d < n; ++d) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, d) != hipSuccess) continue;
+        if (strncmp(prop.gcnArchName, "gfx950", 6) == 0) { g_device = d; break; }
+    }
+    if (g_device < 0) {
+        set_error(-5, "no gfx950 (MI355X) device found");
+        return;
+    }
+    if (hipSetDevice(g_device) != hipSuccess ||
+        hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) {
+        set_error(-7, "cannot open device %d", g_device);
+        return;
+    }
+    g_ok = true;
+}
+
+// Make the backend device current on the calling thread.
+static bool ensure() {
+    std::call_once(g_init_once, init_device);
+    if (!g_ok) return false;
+    static thread_local bool bound = false;
+    if (!bound) {
+        if (hipSetDevice(g_device) != hipSuccess) return false;
+        bound = true;
+    }
+    return true;
+}
+
+bool device_ok() { return ensure(); }
+hipStream_t stream() { return ensure() ? g_stream : nullptr; }
+
+// Serialises multi-kernel entry sequences that share scratch buffers.
+std::mutex g_enqueue_mu;
+
+struct ScratchBuf { void* p = nullptr; size_t n = 0; };
+static ScratchBuf g_scratch[8];
+
+void* scratch(int slot, size_t bytes) {
+    ScratchBuf& b = g_scratch[slot];
+    if (b.n >= bytes) return b.p;
+    (void)hipStreamSynchronize(g_stream);
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.n = 0;
+    size_t want = bytes + bytes / 4 + 256;
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+        set_error(-2, "scratch allocation of %zu bytes failed", want);
+        return nullptr;
+    }
+    b.n = want;
+    return b.p;
+}
+
+void build_rope_table(float* cs, int max_pos, int hd, float theta) {
+    // Same float expressions as llama_infer.c:83-86 (glibc powf/cosf/sinf).
+    const int half = hd / 2;
+    for (int i = 0; i < half; ++i) {
+        float inv_freq = powf(theta, -2.0f * (float)i / (float)hd);
+        for (int p = 0; p < max_pos; ++p) {
+            float ang = (float)p * inv_freq;
+            cs[((size_t)p * half + i) * 2 + 0] = cosf(ang);
+            cs[((size_t)p * half + i) * 2 + 1] = sinf(ang);
+        }
+    }
+}
+
+// Activation buffers for one Q4_K matmul input of B rows x K.
+int make_act16(Act16& a, int B, int K, int slot) {
+    a.rows = B;
+    a.rows_pad = (B + 15) / 16 * 16;
+    a.K = K;
+    size_t nx = (size_t)a.rows_pad * K;
+    size_t ny = (size_t)a.rows_pad * (K / 32) * 2;
+    size_t bytes = nx * 2 * sizeof(_Float16) + ny * sizeof(_Float16) + a.rows_pad * sizeof(float) + 1024;
+    char* p = (char*)scratch(slot, bytes);
+    if (!p) return -2;
+    a.xh = (_Float16*)p;
+    a.xl = a.xh + nx;
+    a.ys = a.xl + nx;
+    size_t off = ((size_t)((char*)(a.ys + ny) - p) + 255) / 256 * 256;
+    a.rinv = (float*)(p + off);
+    return 0;
+}
+
+}  // namespace slate_hip
+
+using namespace slate_hip;
+
+// ===========================================================================
+// C ABI
+extern "C" {
+
+const char* slate_hip_last_error(void) {
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    return g_err_code ? g_err.c_str() : nullptr;
+}
+
+void slate_hip_clear_error(void) {
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    g_err_code = 0;
+    g_err.clear();
+}
+
+void* slate_hip_stream(void) { return (void*)stream(); }
+
+void* slate_hip_alloc(size_t bytes) {
+    if (bytes == 0 || !ensure()) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        set_error(-2, "alloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+void slate_hip_release(void* p) {
+    if (!p || !ensure()) return;
+    (void)hipStreamSynchronize(g_stream);
+    if (hipFree(p) != hipSuccess) set_error(-7, "release(%p) failed", p);
+}
+
+void slate_hip_copy_h2d(void* dst, const void* src, size_t bytes) {
+    if (!bytes || !ensure()) return;
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream) != hipSuccess ||
+        hipStreamSynchronize(g_stream) != hipSuccess)
+        set_error(-7, "copy_h2d(%zu) failed", bytes);
+}
+
+void slate_hip_copy_d2h(void* dst, const void* src, size_t bytes) {
+    if (!bytes || !ensure()) return;
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream) != hipSuccess ||
+        hipStreamSynchronize(g_stream) != hipSuccess)
+        set_error(-7, "copy_d2h(%zu) failed", bytes);
+}
+
+void slate_hip_sync(void) {
+    if (!ensure()) return;
+    hipError_t e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) set_error(-7, "sync failed: %s", hipGetErrorString(e));
+}
+
+void slate_hip_matvec(float* y, const float* A, const float* x, int M, int K) {
+    if (!ensure()) return;
+    if (!y || !A || !x || M <= 0 || K <= 0) { set_error(-1, "matvec: bad arguments"); return; }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    launch_mm_f32(y, x, A, 1, M, K, M, g_stream);
+}
+
+void slate_hip_linear_batch(float* C, const float* X, const float* W, int B, int K, int N) {
+    if (!ensure()) return;
+    if (!C || !X || !W || B <= 0 || K <= 0 || N <= 0) { set_error(-1, "linear_batch: bad arguments"); return; }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    launch_linear_batch(C, X, W, B, K, N, g_stream);
+}
+
+int slate_hip_matmul_q4k(float* Y, const void* A, const float* X, int B, int M, int K) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(Y && A && X && B > 0 && M > 0 && K > 0, "matmul_q4k: bad arguments");
+    SH_REQUIRE(K % QK == 0, "matmul_q4k: K=%d is not a multiple of 256", K);
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    Act16 a;
+    if (make_act16(a, B, K, 0)) return -2;
+    int rc = launch_act16_from_f32(a, X, g_stream);
+    if (rc) return rc;
+    int S = q4k_pick_splits(M, K, a.rows_pad);
+    float* part = (float*)scratch(1, (size_t)S * a.rows_pad * M * sizeof(float));
+    if (!part) return -2;
+    rc = launch_q4k_mm(A, a, part, (int64_t)M, (int64_t)a.rows_pad * M, M, S, g_stream);
+    if (rc) return rc;
+    return launch_sum_splits(Y, part, S, B, a.rows_pad, M, g_stream);
+}
+
+void slate_hip_matvec_q4k(float* y, const void* A, const float* x, int M, int K) {
+    slate_hip_matmul_q4k(y, A, x, 1, M, K);
+}
+
+int slate_hip_dequant_q4k(float* dst, const void* A, int64_t n) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(dst && A && n >= 0 && n % QK == 0, "dequant_q4k: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_dequant_q4k(dst, A, n / QK, g_stream);
+}
+
+int slate_hip_rmsnorm_rows(float* y, const float* x, const float* w, int B, int D, float eps) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(y && x && w && B > 0 && D > 0, "rmsnorm_rows: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_rmsnorm_rows(y, (float*)x, nullptr, 1, 0, w, B, D, eps, g_stream);
+}
+
+void slate_hip_rmsnorm_row(float* y, const float* x, const float* w, int D, float eps) {
+    slate_hip_rmsnorm_rows(y, x, w, 1, D, eps);
+}
+
+void slate_hip_silu_mul(float* y, const float* gate, const float* up, int H) {
+    if (!ensure()) return;
+    if (!y || !gate || !up || H <= 0) { set_error(-1, "silu_mul: bad arguments"); return; }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    launch_silu_mul(y, gate, up, 1, H, 1, 0, H, H, g_stream);
+}
+
+void slate_hip_add_inplace(float* y, const float* x, int D) {
+    if (!ensure()) return;
+    if (!y || !x || D < 0) { set_error(-1, "add_inplace: bad arguments"); return; }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    launch_add(y, x, D, g_stream);
+}
+
+void slate_hip_embed_lookup(float* y, const float* W, int token_id, int D) {
+    if (!ensure()) return;
+    if (!y || !W || token_id < 0 || D <= 0) { set_error(-1, "embed_lookup: bad arguments"); return; }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    if (hipMemcpyAsync(y, W + (int64_t)token_id * D, (size_t)D * sizeof(float), hipMemcpyDeviceToDevice,
+                       g_stream) != hipSuccess)
+        set_error(-7, "embed_lookup copy failed");
+}
+
+void slate_hip_attention_step(float* out, const float* q, const float* K, const float* V, float* scores,
+                              int L, int D) {
+    if (!ensure()) return;
+    if (!out || !q || !K || !V || !scores || L <= 0 || D <= 0) {
+        set_error(-1, "attention_step: bad arguments");
+        return;
+    }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    launch_attention_step(out, q, K, V, scores, L, D, g_stream);
+}
+
+int slate_hip_argmax_rows(int32_t* out, const float* logits, int B, int V) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(out && logits && B > 0 && V > 0, "argmax_rows: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_argmax_rows(out, logits, B, V, g_stream);
+}
+
+struct RopeTable { float* dev = nullptr; int max_pos = 0; };
+static std::map<std::pair<int, uint32_t>, RopeTable> g_rope;
+
+int slate_hip_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int head_dim,
+                        float theta_base, int max_pos) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(x && pos && n_rows > 0 && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && max_pos > 0,
+               "rope_rows: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    uint32_t tb;
+    memcpy(&tb, &theta_base, 4);
+    RopeTable& t = g_rope[{head_dim, tb}];
+    if (t.max_pos < max_pos) {
+        std::vector<float> host((size_t)max_pos * head_dim);
+        build_rope_table(host.data(), max_pos, head_dim, theta_base);
+        (void)hipStreamSynchronize(g_stream);
+        if (t.dev) (void)hipFree(t.dev);
+        t.dev = nullptr;
+        t.max_pos = 0;
+        SH_CHECK_HIP(hipMalloc(&t.dev, host.size() * sizeof(float)));
+        SH_CHECK_HIP(hipMemcpy(t.dev, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice));
+        t.max_pos = max_pos;
+    }
+    int* bad = (int*)scratch(2, 256);
+    if (!bad) return -2;
+    SH_CHECK_HIP(hipMemsetAsync(bad, 0, sizeof(int), g_stream));
+    int rc = launch_rope_rows(x, pos, n_rows, n_heads, head_dim, t.dev, max_pos, bad, g_stream);
+    if (rc) return rc;
+    int hbad = 0;
+    SH_CHECK_HIP(hipMemcpyAsync(&hbad, bad, sizeof(int), hipMemcpyDeviceToHost, g_stream));
+    SH_CHECK_HIP(hipStreamSynchronize(g_stream));
+    SH_REQUIRE(hbad == 0, "rope_rows: %d rows with |pos| >= max_pos=%d left unrotated", hbad, max_pos);
+    return 0;
+}
+
+void slate_hip_rope_table(float* cs, int max_pos, int head_dim, float theta_base) {
+    build_rope_table(cs, max_pos, head_dim, theta_base);
+}
+
+int slate_hip_pack_batch(const int32_t* slot, const int32_t* pos0, const int32_t* n_new, int B, int max_seq,
+                         int64_t slot_stride, int T_cap, int32_t* tok_off, int32_t* tok2seq, int32_t* tok_pos,
+                         int64_t* kv_base, int32_t* last_tok, int32_t* status) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(slot && pos0 && n_new && B >= 1 && B <= 1024 && tok_off && tok2seq && tok_pos && kv_base &&
+                   last_tok && status && T_cap >= 1,
+               "pack_batch: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_pack_batch(slot, pos0, n_new, B, max_seq, slot_stride, T_cap, tok_off, tok2seq, tok_pos,
+                             kv_base, last_tok, status, g_stream);
+}
+
+int slate_hip_attention_ragged(float* out, const float* q, const float* Kpool, const float* Vpool,
+                               const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
+                               int n_q_heads, int n_kv_heads, int head_dim, int64_t head_stride, int max_pos) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(out && q && Kpool && Vpool && tok2seq && tok_pos && kv_base && T > 0 && max_pos > 0,
+               "attention_ragged: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    size_t nf = attention_partial_floats(T, n_q_heads, head_dim, max_pos);
+    float* po = (float*)scratch(3, nf * sizeof(float));
+    if (!po) return -2;
+    float* pml = po + (size_t)T * n_q_heads * ((max_pos + attn_chunk_size() - 1) / attn_chunk_size()) * head_dim;
+    return launch_attention_ragged(out, q, Kpool, Vpool, tok2seq, tok_pos, kv_base, T, n_q_heads, n_kv_heads,
+                                   head_dim, head_stride, max_pos, po, pml, g_stream);
+}
+
+int slate_hip_synth_f32(float* dst, int64_t n, uint64_t seed, float std) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(dst && n >= 0, "synth_f32: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_synth_f32(dst, n, seed, std, 0.f, g_stream);
+}
+
+int slate_hip_synth_q4k(void* dst, int64_t rows, int64_t cols, uint64_t seed, float std) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(dst && rows >= 0 && cols > 0, "synth_q4k: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_synth_q4k(dst, rows, cols, seed, std, g_stream);
+}
+
+static const char* hip_last_error_entry(void) { return slate_hip_last_error(); }
+
+static slate_hip_backend_t g_vtable = {
+    {
+        "hip",
+        slate_hip_alloc,
+        slate_hip_release,
+        slate_hip_copy_h2d,
+        slate_hip_copy_d2h,
+        slate_hip_matvec,
+        slate_hip_linear_batch,
+        slate_hip_matvec_q4k,
+        slate_hip_rmsnorm_row,
+        slate_hip_silu_mul,
+        slate_hip_add_inplace,
+        slate_hip_embed_lookup,
+        slate_hip_attention_step,
+        slate_hip_sync,
+    },
+    slate_hip_matmul_q4k,
+    slate_hip_dequant_q4k,
+    slate_hip_rmsnorm_rows,
+    slate_hip_rope_rows,
+    slate_hip_argmax_rows,
+    hip_last_error_entry,
+};
+
+const slate_backend_t* slate_backend_hip(void) {
+    if (!ensure()) return nullptr;
+    return &g_vtable.base;
+}
+
+}  // extern "C"

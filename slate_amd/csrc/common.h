@@ -1,0 +1,75 @@
+// common.h -- shared host/device definitions for the gfx950 backend.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/slate_hip.h"
+
+namespace slate_hip {
+
+// ---------------------------------------------------------------------------
+// Errors: a sticky process-wide message (compute entries return void at the
+// vtable boundary, so failures must be observable afterwards).
+void set_error(int code, const char* fmt, ...);
+int  error_code();
+hipStream_t stream();        // the backend stream (created on first use)
+bool device_ok();            // a gfx950 device was opened
+
+#define SH_CHECK_HIP(expr)                                                        \
+    do {                                                                          \
+        hipError_t _e = (expr);                                                   \
+        if (_e != hipSuccess) {                                                   \
+            ::slate_hip::set_error(-7, "%s failed: %s (%s:%d)", #expr,            \
+                                   hipGetErrorString(_e), __FILE__, __LINE__);    \
+            return -7;                                                            \
+        }                                                                         \
+    } while (0)
+
+#define SH_CHECK_LAUNCH() SH_CHECK_HIP(hipGetLastError())
+
+#define SH_REQUIRE(cond, ...)                                                     \
+    do {                                                                          \
+        if (!(cond)) { ::slate_hip::set_error(-1, __VA_ARGS__); return -1; }      \
+    } while (0)
+
+// Scratch owned by the backend: grown on demand, reused across calls.  Every
+// use happens on the single backend stream, so reuse is ordered.
+void* scratch(int slot, size_t bytes);
+
+// ---------------------------------------------------------------------------
+// Q4_K super-block geometry (include/slate/quant.h:34-36).
+constexpr int QK = 256;
+constexpr int QBLOCK = 144;
+
+// Activation operand for the Q4_K MFMA kernels: X split into f16 hi + lo with
+// a per-row power-of-two scale, plus per-32-element sums for the min term.
+//   xh, xl : [rows_pad][K]      f16     (x * rscale = hi + lo)
+//   ys     : [rows_pad][K/32][2] f16    (hi, lo) of sum over each sub-block
+//   rinv   : [rows_pad]          f32    1 / rscale
+struct Act16 {
+    _Float16* xh;
+    _Float16* xl;
+    _Float16* ys;
+    float* rinv;
+    int rows;       // valid rows
+    int rows_pad;   // multiple of 16
+    int K;
+};
+
+// Launchers (all enqueue on the given stream; return 0 or negative code).
+int launch_dequant_q4k(float* dst, const void* src, int64_t n_blocks, hipStream_t s);
+int launch_act16_from_f32(const Act16& a, const float* X, hipStream_t s);
+// Split-K partial outputs: element (split, row b, col m) is written to
+// out[split * split_stride + b * ldo + m] for b < rows_pad; with nsplit == 1
+// the single partial is the result.
+int launch_q4k_mm(const void* W, const Act16& a, float* out, int64_t ldo, int64_t split_stride, int M,
+                  int nsplit, hipStream_t s);
+int launch_sum_splits(float* Y, const float* part, int nsplit, int rows, int rows_pad, int M,
+                      hipStream_t s);
+int q4k_pick_splits(int M, int K, int rows_pad);
+// Carve an Act16 for B rows x K out of backend scratch slot `slot`.
+int make_act16(Act16& a, int B, int K, int slot);
+
+}  // namespace slate_hip

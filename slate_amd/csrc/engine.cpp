@@ -1,0 +1,635 @@
+// engine.cpp -- device-resident LLaMA engine with a ragged continuous-batching
+// step.  Per-token semantics are those of decode_one (llama_infer.c:134-206);
+// the batched step generalises slate_infer_batch_step (engine.c:543-642) to
+// LLaMA and to sequences contributing several tokens in one step (prefill
+// chunks mixed with decode rows).
+//
+// HBM layout:
+//   weights       as given (Q4_K rows of 144-byte blocks, or f32 [out, in])
+//   K/V pools     [slot][layer][kv_head][max_seq][head_dim] f32
+//   RoPE table    [max_seq][head_dim/2][2] f32 (host-computed angles)
+//   activations   [T][...] f32, packed token-major; split-K partials
+//                 [split][T_pad][width]
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "launch.h"
+
+namespace slate_hip {
+extern std::mutex g_enqueue_mu;
+}
+using namespace slate_hip;
+
+namespace {
+
+constexpr int DT_F32 = 0;
+constexpr int DT_Q4K = 18;
+
+struct Lin {
+    void* w = nullptr;
+    int dtype = DT_F32;
+    int M = 0, K = 0;
+    size_t bytes() const {
+        return dtype == DT_Q4K ? (size_t)M * (K / QK) * QBLOCK : (size_t)M * K * sizeof(float);
+    }
+};
+
+struct LayerDev {
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    Lin q, k, v, o, gate, up, down;
+};
+
+}  // namespace
+
+struct slate_hip_llama {
+    slate_hip_llama_config_t cfg{};
+    int max_slots = 0, max_tokens = 0, tpad_cap = 0;
+    float* tok_embd = nullptr;
+    float* out_norm = nullptr;
+    Lin out;
+    std::vector<LayerDev> L;
+    float *Kpool = nullptr, *Vpool = nullptr;
+    int64_t slot_stride = 0, layer_stride = 0, head_stride = 0;
+    float* rope_cs = nullptr;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr;
+    float *xlast = nullptr, *logits = nullptr;
+    float* part = nullptr;
+    size_t part_floats = 0;
+    float *att_po = nullptr, *att_pml = nullptr;
+    Act16 act{};
+    int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
+            *last_tok = nullptr, *status = nullptr, *next = nullptr;
+    int64_t* kv_base = nullptr;
+    int32_t *h_desc = nullptr, *h_tok = nullptr, *h_next = nullptr, *h_status = nullptr;
+    float* h_logits = nullptr;
+    std::vector<int> free_slots;
+    std::vector<void*> allocs;
+    std::mutex mu;
+};
+
+struct slate_hip_llama_session {
+    slate_hip_llama* m;
+    int slot;
+    int pos;
+};
+
+namespace {
+
+template <class T>
+int dalloc(slate_hip_llama* m, T** p, size_t count) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    void* v = nullptr;
+    if (hipMalloc(&v, count * sizeof(T)) != hipSuccess) {
+        set_error(-2, "engine: device allocation of %zu bytes failed", count * sizeof(T));
+        return -2;
+    }
+    m->allocs.push_back(v);
+    *p = (T*)v;
+    return 0;
+}
+
+void free_model(slate_hip_llama* m) {
+    if (!m) return;
+    (void)hipStreamSynchronize(stream());
+    for (void* p : m->allocs) (void)hipFree(p);
+    if (m->h_desc) (void)hipHostFree(m->h_desc);
+    if (m->h_tok) (void)hipHostFree(m->h_tok);
+    if (m->h_next) (void)hipHostFree(m->h_next);
+    if (m->h_status) (void)hipHostFree(m->h_status);
+    if (m->h_logits) (void)hipHostFree(m->h_logits);
+    delete m;
+}
+
+bool valid_cfg(const slate_hip_llama_config_t* c) {
+    return c && c->n_layers > 0 && c->d_model > 0 && c->ffn_hidden > 0 && c->n_heads > 0 && c->n_kv_heads > 0 &&
+           c->n_heads % c->n_kv_heads == 0 && c->head_dim > 0 && c->head_dim % 2 == 0 &&
+           c->n_heads * c->head_dim == c->d_model && c->max_seq > 0 && c->vocab > 0;
+}
+
+// Allocate everything but the weights.
+int alloc_runtime(slate_hip_llama* m) {
+    const auto& c = m->cfg;
+    const int D = c.d_model, H = c.ffn_hidden, kvd = c.n_kv_heads * c.head_dim;
+    m->tpad_cap = (m->max_tokens + 15) / 16 * 16;
+    m->head_stride = (int64_t)c.max_seq * c.head_dim;
+    m->layer_stride = (int64_t)c.n_kv_heads * m->head_stride;
+    m->slot_stride = (int64_t)c.n_layers * m->layer_stride;
+    size_t kv = (size_t)m->max_slots * m->slot_stride;
+    if (dalloc(m, &m->Kpool, kv) || dalloc(m, &m->Vpool, kv)) return -2;
+    // RoPE table with the reference's float angle expressions.
+    {
+        std::vector<float> cs((size_t)c.max_seq * c.head_dim);
+        build_rope_table(cs.data(), c.max_seq, c.head_dim, c.theta_base);
+        if (dalloc(m, &m->rope_cs, cs.size())) return -2;
+        if (hipMemcpy(m->rope_cs, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) {
+            set_error(-7, "engine: rope table upload failed");
+            return -7;
+        }
+    }
+    const size_t T = m->tpad_cap;
+    if (dalloc(m, &m->x, T * D) || dalloc(m, &m->xn, T * D) || dalloc(m, &m->q, T * D) ||
+        dalloc(m, &m->att, T * D) || dalloc(m, &m->h, T * H) || dalloc(m, &m->xlast, (size_t)m->max_slots * D) ||
+        // the LM-head matmul writes whole 16-row tiles
+        dalloc(m, &m->logits, (size_t)((m->max_slots + 15) / 16 * 16) * c.vocab))
+        return -2;
+    const int W = std::max({D + 2 * kvd, 2 * H, D});
+    m->part_floats = (size_t)std::max<size_t>(16 * 64, T) * W;
+    if (dalloc(m, &m->part, m->part_floats)) return -2;
+    size_t np = attention_partial_floats((int)T, c.n_heads, c.head_dim, c.max_seq);
+    if (dalloc(m, &m->att_po, np)) return -2;
+    m->att_pml = m->att_po + (size_t)T * c.n_heads * ((c.max_seq + attn_chunk_size() - 1) / attn_chunk_size()) *
+                                 c.head_dim;
+    // Act16 buffers for the widest matmul input (max(D, H)), T_pad rows
+    const int Kmax = std::max(D, H);
+    Act16& a = m->act;
+    a.K = Kmax;
+    if (dalloc(m, &a.xh, T * Kmax) || dalloc(m, &a.xl, T * Kmax) || dalloc(m, &a.ys, T * (Kmax / 32 + 1) * 2) ||
+        dalloc(m, &a.rinv, T))
+        return -2;
+    const int S = m->max_slots;
+    if (dalloc(m, &m->d_desc, 3 * (size_t)S) || dalloc(m, &m->d_tok, T) || dalloc(m, &m->tok_off, S + 1) ||
+        dalloc(m, &m->tok2seq, T) || dalloc(m, &m->tok_pos, T) || dalloc(m, &m->last_tok, S) ||
+        dalloc(m, &m->status, 4) || dalloc(m, &m->next, S) || dalloc(m, &m->kv_base, S))
+        return -2;
+    if (hipHostMalloc((void**)&m->h_desc, 3 * sizeof(int32_t) * S) != hipSuccess ||
+        hipHostMalloc((void**)&m->h_tok, sizeof(int32_t) * T) != hipSuccess ||
+        hipHostMalloc((void**)&m->h_next, sizeof(int32_t) * S) != hipSuccess ||
+        hipHostMalloc((void**)&m->h_status, sizeof(int32_t) * 4) != hipSuccess ||
+        hipHostMalloc((void**)&m->h_logits, sizeof(float) * (size_t)S * c.vocab) != hipSuccess) {
+        set_error(-2, "engine: pinned host allocation failed");
+        return -2;
+    }
+    // KV pools start zeroed, like calloc in llama_infer.c:225-226
+    if (hipMemset(m->Kpool, 0, kv * sizeof(float)) != hipSuccess ||
+        hipMemset(m->Vpool, 0, kv * sizeof(float)) != hipSuccess) {
+        set_error(-7, "engine: KV clear failed");
+        return -7;
+    }
+    // the clears and uploads above run outside the backend stream: finish them
+    if (hipDeviceSynchronize() != hipSuccess) {
+        set_error(-7, "engine: device synchronisation failed");
+        return -7;
+    }
+    for (int i = S - 1; i >= 0; --i) m->free_slots.push_back(i);
+    return 0;
+}
+
+int upload(slate_hip_llama* m, void** dst, const void* src, size_t bytes) {
+    if (!src) {
+        set_error(-1, "engine: missing weight pointer");
+        return -1;
+    }
+    char* p;
+    if (dalloc(m, &p, bytes)) return -2;
+    if (hipMemcpy(p, src, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        set_error(-7, "engine: weight upload failed");
+        return -7;
+    }
+    *dst = p;
+    return 0;
+}
+
+int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int K) {
+    l.M = M;
+    l.K = K;
+    l.dtype = dtype;
+    if (dtype != DT_F32 && dtype != DT_Q4K) {
+        set_error(-5, "engine: weight dtype %d not supported (f32=0, q4_k=18)", dtype);
+        return -5;
+    }
+    if (dtype == DT_Q4K && K % QK) {
+        set_error(-1, "engine: Q4_K weight with K=%d (not a multiple of 256)", K);
+        return -1;
+    }
+    return upload(m, &l.w, host, l.bytes());
+}
+
+// One matmul group: the linears in `lins` read the same input X [T, K] and
+// write column ranges of one partial buffer [S][T_pad][ldo].  Returns S.
+int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const* lins, const int64_t* col,
+             int nl, int64_t ldo, int* S_out, hipStream_t s) {
+    bool anyq = false, anyf = false;
+    int Mtot = 0;
+    for (int i = 0; i < nl; ++i) {
+        anyq |= lins[i]->dtype == DT_Q4K;
+        anyf |= lins[i]->dtype == DT_F32;
+        Mtot += lins[i]->M;
+    }
+    const int tpad = (T + 15) / 16 * 16;
+    int S = 1;
+    Act16 a = m->act;
+    a.rows = T;
+    a.rows_pad = tpad;
+    a.K = K;
+    if (anyq) {
+        int rc = launch_act16_from_f32(a, X, s);
+        if (rc) return rc;
+        if (!anyf) {
+            S = q4k_pick_splits(Mtot, K, tpad);
+            while (S > 1 && (size_t)S * tpad * ldo > m->part_floats) --S;
+        }
+    }
+    const int64_t ss = (int64_t)tpad * ldo;
+    for (int i = 0; i < nl; ++i) {
+        const Lin& l = *lins[i];
+        int rc = l.dtype == DT_Q4K ? launch_q4k_mm(l.w, a, m->part + col[i], ldo, ss, l.M, S, s)
+                                   : launch_mm_f32(m->part + col[i], X, (const float*)l.w, T, l.M, K, (int)ldo, s);
+        if (rc) return rc;
+    }
+    *S_out = S;
+    return 0;
+}
+
+// Final projection for n rows into m->logits [n][V] (single split).
+int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
+    const auto& c = m->cfg;
+    const Lin& l = m->out;
+    if (l.dtype == DT_Q4K) {
+        Act16 a = m->act;
+        a.rows = n;
+        a.rows_pad = (n + 15) / 16 * 16;
+        a.K = c.d_model;
+        int rc = launch_act16_from_f32(a, m->xlast, s);
+        if (rc) return rc;
+        return launch_q4k_mm(l.w, a, m->logits, c.vocab, 0, c.vocab, 1, s);
+    }
+    return launch_mm_f32(m->logits, m->xlast, (const float*)l.w, n, c.vocab, c.d_model, c.vocab, s);
+}
+
+// Enqueue the whole step (descriptors already in pinned staging).
+int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t s) {
+    const auto& c = m->cfg;
+    const int D = c.d_model, H = c.ffn_hidden, hd = c.head_dim, kvd = c.n_kv_heads * hd;
+    SH_CHECK_HIP(hipMemcpyAsync(m->d_desc, m->h_desc, 3 * sizeof(int32_t) * m->max_slots, hipMemcpyHostToDevice, s));
+    SH_CHECK_HIP(hipMemcpyAsync(m->d_tok, m->h_tok, sizeof(int32_t) * T, hipMemcpyHostToDevice, s));
+    int rc = launch_pack_batch(m->d_desc, m->d_desc + m->max_slots, m->d_desc + 2 * m->max_slots, n, c.max_seq,
+                               m->slot_stride, m->max_tokens, m->tok_off, m->tok2seq, m->tok_pos, m->kv_base,
+                               m->last_tok, m->status, s);
+    if (rc) return rc;
+    if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
+    const int tpad = (T + 15) / 16 * 16;
+    int S_prev = 0;
+    for (int li = 0; li < c.n_layers; ++li) {
+        const LayerDev& Ld = m->L[li];
+        // x (+= down partials of the previous layer) -> xn
+        if ((rc = launch_rmsnorm_rows(m->xn, m->x, li ? m->part : nullptr, S_prev, (int64_t)tpad * D,
+                                      Ld.attn_norm, T, D, c.rms_eps, s)))
+            return rc;
+        int S;
+        {
+            const Lin* g[3] = {&Ld.q, &Ld.k, &Ld.v};
+            int64_t col[3] = {0, D, D + kvd};
+            if ((rc = mm_group(m, m->xn, T, D, g, col, 3, D + 2 * kvd, &S, s))) return rc;
+        }
+        float* Kl = m->Kpool + (int64_t)li * m->layer_stride;
+        float* Vl = m->Vpool + (int64_t)li * m->layer_stride;
+        if ((rc = launch_rope_kv_append(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
+                                        m->tok2seq, m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd,
+                                        m->head_stride, m->rope_cs, s)))
+            return rc;
+        if ((rc = launch_attention_ragged(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, c.n_heads,
+                                          c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po, m->att_pml, s)))
+            return rc;
+        {
+            const Lin* g[1] = {&Ld.o};
+            int64_t col[1] = {0};
+            if ((rc = mm_group(m, m->att, T, D, g, col, 1, D, &S, s))) return rc;
+        }
+        if ((rc = launch_rmsnorm_rows(m->xn, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm, T, D, c.rms_eps, s)))
+            return rc;
+        {
+            const Lin* g[2] = {&Ld.gate, &Ld.up};
+            int64_t col[2] = {0, H};
+            if ((rc = mm_group(m, m->xn, T, D, g, col, 2, 2 * H, &S, s))) return rc;
+        }
+        if ((rc = launch_silu_mul(m->h, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H, 2 * H, 2 * H, s)))
+            return rc;
+        {
+            const Lin* g[1] = {&Ld.down};
+            int64_t col[1] = {0};
+            if ((rc = mm_group(m, m->h, T, H, g, col, 1, D, &S, s))) return rc;
+        }
+        S_prev = S;
+    }
+    if ((rc = launch_rmsnorm_rows(m->xn, m->x, m->part, S_prev, (int64_t)tpad * D, m->out_norm, T, D, c.rms_eps, s)))
+        return rc;
+    // rows of each sequence's last token -> xlast (gather by last_tok)
+    if ((rc = launch_embed_rows(m->xlast, m->xn, m->last_tok, n, T, D, s))) return rc;
+    if ((rc = lm_head(m, n, s))) return rc;
+    if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, s))) return rc;
+    SH_CHECK_HIP(hipMemcpyAsync(m->h_next, m->next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
+    SH_CHECK_HIP(hipMemcpyAsync(m->h_status, m->status, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    if (want_logits)
+        SH_CHECK_HIP(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * (size_t)n * c.vocab,
+                                    hipMemcpyDeviceToHost, s));
+    return 0;
+}
+
+int new_common(slate_hip_llama* m, const slate_hip_llama_config_t* cfg, int max_slots, int max_tokens) {
+    if (!valid_cfg(cfg)) {
+        set_error(-1, "engine: invalid config");
+        return -1;
+    }
+    if (max_slots < 1 || max_slots > 1024 || max_tokens < max_slots) {
+        set_error(-1, "engine: need 1 <= max_slots <= 1024 and max_tokens >= max_slots");
+        return -1;
+    }
+    m->cfg = *cfg;
+    m->max_slots = max_slots;
+    m->max_tokens = max_tokens;
+    return alloc_runtime(m);
+}
+
+uint64_t mix(uint64_t a, uint64_t b) {
+    uint64_t z = a * 0x9E3779B97F4A7C15ull + b;
+    z = (z ^ (z >> 31)) * 0xBF58476D1CE4E5B9ull;
+    return z ^ (z >> 29);
+}
+
+}  // namespace
+
+extern "C" {
+
+slate_hip_llama_t* slate_hip_llama_new(const slate_hip_llama_config_t* cfg, const float* token_embd,
+                                       const float* output_norm, const void* output, int output_dtype,
+                                       const slate_hip_llama_layer_t* layers, int max_slots, int max_tokens) {
+    if (!device_ok()) return nullptr;
+    if (!token_embd || !output_norm || !layers) {
+        set_error(-1, "llama_new: NULL weights");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    slate_hip_llama* m = new slate_hip_llama();
+    if (new_common(m, cfg, max_slots, max_tokens)) { free_model(m); return nullptr; }
+    const auto& c = m->cfg;
+    const int D = c.d_model, H = c.ffn_hidden, kvd = c.n_kv_heads * c.head_dim;
+    void* p;
+    if (upload(m, &p, token_embd, (size_t)c.vocab * D * 4)) { free_model(m); return nullptr; }
+    m->tok_embd = (float*)p;
+    if (upload(m, &p, output_norm, (size_t)D * 4)) { free_model(m); return nullptr; }
+    m->out_norm = (float*)p;
+    if (!output || c.tied_output) {   // tied LM head (llama.c:94-101)
+        m->out.w = m->tok_embd;
+        m->out.dtype = DT_F32;
+        m->out.M = c.vocab;
+        m->out.K = D;
+    } else if (set_lin(m, m->out, output, output_dtype, c.vocab, D)) {
+        free_model(m);
+        return nullptr;
+    }
+    m->L.resize(c.n_layers);
+    for (int i = 0; i < c.n_layers; ++i) {
+        const slate_hip_llama_layer_t& s = layers[i];
+        LayerDev& d = m->L[i];
+        if (upload(m, &p, s.attn_norm, (size_t)D * 4)) { free_model(m); return nullptr; }
+        d.attn_norm = (float*)p;
+        if (upload(m, &p, s.ffn_norm, (size_t)D * 4)) { free_model(m); return nullptr; }
+        d.ffn_norm = (float*)p;
+        if (set_lin(m, d.q, s.attn_q, s.attn_q_dtype, D, D) || set_lin(m, d.k, s.attn_k, s.attn_k_dtype, kvd, D) ||
+            set_lin(m, d.v, s.attn_v, s.attn_v_dtype, kvd, D) ||
+            set_lin(m, d.o, s.attn_output, s.attn_output_dtype, D, D) ||
+            set_lin(m, d.gate, s.ffn_gate, s.ffn_gate_dtype, H, D) || set_lin(m, d.up, s.ffn_up, s.ffn_up_dtype, H, D) ||
+            set_lin(m, d.down, s.ffn_down, s.ffn_down_dtype, D, H)) {
+            free_model(m);
+            return nullptr;
+        }
+    }
+    return m;
+}
+
+slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t* cfg, uint64_t seed, int quant,
+                                                 int max_slots, int max_tokens) {
+    if (!device_ok()) return nullptr;
+    if (quant != DT_F32 && quant != DT_Q4K) {
+        set_error(-1, "llama_new_synthetic: quant must be 0 (f32) or 18 (q4_k)");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    slate_hip_llama* m = new slate_hip_llama();
+    if (new_common(m, cfg, max_slots, max_tokens)) { free_model(m); return nullptr; }
+    const auto& c = m->cfg;
+    const int D = c.d_model, H = c.ffn_hidden, kvd = c.n_kv_heads * c.head_dim;
+    hipStream_t s = stream();
+    uint64_t tid = 0;
+    const float std = 0.02f;
+    auto gen_lin = [&](Lin& l, int M, int K) -> int {
+        l.M = M;
+        l.K = K;
+        l.dtype = quant;
+        if (quant == DT_Q4K && K % QK) {
+            set_error(-1, "llama_new_synthetic: K=%d not a multiple of 256", K);
+            return -1;
+        }
+        char* p;
+        if (dalloc(m, &p, l.bytes())) return -2;
+        l.w = p;
+        uint64_t sd = mix(seed, ++tid);
+        return quant == DT_Q4K ? launch_synth_q4k(p, M, K, sd, std, s)
+                               : launch_synth_f32((float*)p, (int64_t)M * K, sd, std, 0.f, s);
+    };
+    auto gen_f32 = [&](float** dst, int64_t n, float sd_std, float fill) -> int {
+        if (dalloc(m, dst, (size_t)n)) return -2;
+        return launch_synth_f32(*dst, n, mix(seed, ++tid), sd_std, fill, s);
+    };
+    int rc = gen_f32(&m->tok_embd, (int64_t)c.vocab * D, std, 0.f);
+    rc = rc ? rc : gen_f32(&m->out_norm, D, 0.f, 1.0f);
+    rc = rc ? rc : gen_lin(m->out, c.vocab, D);
+    m->L.resize(c.n_layers);
+    for (int i = 0; i < c.n_layers && !rc; ++i) {
+        LayerDev& d = m->L[i];
+        rc = gen_f32(&d.attn_norm, D, 0.f, 1.0f);
+        rc = rc ? rc : gen_f32(&d.ffn_norm, D, 0.f, 1.0f);
+        rc = rc ? rc : gen_lin(d.q, D, D);
+        rc = rc ? rc : gen_lin(d.k, kvd, D);
+        rc = rc ? rc : gen_lin(d.v, kvd, D);
+        rc = rc ? rc : gen_lin(d.o, D, D);
+        rc = rc ? rc : gen_lin(d.gate, H, D);
+        rc = rc ? rc : gen_lin(d.up, H, D);
+        rc = rc ? rc : gen_lin(d.down, D, H);
+    }
+    if (!rc && hipStreamSynchronize(s) != hipSuccess) {
+        set_error(-7, "llama_new_synthetic: generation failed");
+        rc = -7;
+    }
+    if (rc) { free_model(m); return nullptr; }
+    return m;
+}
+
+void slate_hip_llama_free(slate_hip_llama_t* m) {
+    if (!m) return;
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    free_model(m);
+}
+
+int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name, void* host_dst, int64_t cap,
+                                   int* dtype) {
+    if (!m || !name) return -1;
+    const void* src = nullptr;
+    size_t bytes = 0;
+    int dt = DT_F32;
+    const auto& c = m->cfg;
+    std::string n(name);
+    if (n == "token_embd") { src = m->tok_embd; bytes = (size_t)c.vocab * c.d_model * 4; }
+    else if (n == "output_norm") { src = m->out_norm; bytes = (size_t)c.d_model * 4; }
+    else if (n == "output") { src = m->out.w; bytes = m->out.bytes(); dt = m->out.dtype; }
+    else if (n.rfind("blk.", 0) == 0) {
+        int li = atoi(n.c_str() + 4);
+        size_t dot = n.find('.', 4);
+        if (li < 0 || li >= c.n_layers || dot == std::string::npos) return -1;
+        std::string f = n.substr(dot + 1);
+        const LayerDev& d = m->L[li];
+        const Lin* l = nullptr;
+        if (f == "attn_norm") { src = d.attn_norm; bytes = (size_t)c.d_model * 4; }
+        else if (f == "ffn_norm") { src = d.ffn_norm; bytes = (size_t)c.d_model * 4; }
+        else if (f == "attn_q") l = &d.q;
+        else if (f == "attn_k") l = &d.k;
+        else if (f == "attn_v") l = &d.v;
+        else if (f == "attn_output") l = &d.o;
+        else if (f == "ffn_gate") l = &d.gate;
+        else if (f == "ffn_up") l = &d.up;
+        else if (f == "ffn_down") l = &d.down;
+        else return -1;
+        if (l) { src = l->w; bytes = l->bytes(); dt = l->dtype; }
+    } else {
+        return -1;
+    }
+    if (dtype) *dtype = dt;
+    if (!host_dst) return (int64_t)bytes;
+    if ((int64_t)bytes > cap) return -2;
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    if (hipStreamSynchronize(stream()) != hipSuccess ||
+        hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+        set_error(-7, "get_tensor copy failed");
+        return -7;
+    }
+    return (int64_t)bytes;
+}
+
+slate_hip_llama_session_t* slate_hip_llama_session_new(slate_hip_llama_t* m) {
+    if (!m) return nullptr;
+    std::lock_guard<std::mutex> lk(m->mu);
+    if (m->free_slots.empty()) {
+        set_error(-2, "session_new: all %d KV slots in use", m->max_slots);
+        return nullptr;
+    }
+    auto* s = new slate_hip_llama_session{m, m->free_slots.back(), 0};
+    m->free_slots.pop_back();
+    return s;
+}
+
+void slate_hip_llama_session_free(slate_hip_llama_session_t* s) {
+    if (!s) return;
+    {
+        std::lock_guard<std::mutex> lk(s->m->mu);
+        s->m->free_slots.push_back(s->slot);
+    }
+    delete s;
+}
+
+int slate_hip_llama_session_position(const slate_hip_llama_session_t* s) { return s ? s->pos : -1; }
+
+int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessions, int n, const int32_t* n_new,
+                         const int32_t* tokens, float* out_logits, int32_t* out_next) {
+    if (!m || !sessions || !n_new || !tokens || n < 1 || n > m->max_slots) return -1;
+    const auto& c = m->cfg;
+    std::lock_guard<std::mutex> lk(m->mu);
+    int T = 0;
+    for (int i = 0; i < n; ++i) {
+        slate_hip_llama_session_t* s = sessions[i];
+        if (!s || s->m != m || n_new[i] < 1) return -1;
+        for (int j = 0; j < i; ++j)
+            if (sessions[j] == s) return -1;
+        if ((int64_t)s->pos + n_new[i] > c.max_seq) return -2;
+        T += n_new[i];
+        if (T > m->max_tokens) return -2;
+    }
+    for (int t = 0; t < T; ++t)
+        if (tokens[t] < 0 || tokens[t] >= c.vocab) return -3;
+    for (int i = 0; i < m->max_slots; ++i) {
+        bool act = i < n;
+        m->h_desc[i] = act ? sessions[i]->slot : 0;
+        m->h_desc[m->max_slots + i] = act ? sessions[i]->pos : 0;
+        m->h_desc[2 * m->max_slots + i] = act ? n_new[i] : 0;
+    }
+    memcpy(m->h_tok, tokens, sizeof(int32_t) * T);
+    hipStream_t s = stream();
+    {
+        std::lock_guard<std::mutex> lk2(g_enqueue_mu);
+        int rc = enqueue_step(m, n, T, out_logits != nullptr, s);
+        if (rc) return rc;
+        if (hipStreamSynchronize(s) != hipSuccess) {
+            set_error(-7, "llama_step: device execution failed");
+            return -7;
+        }
+    }
+    if (m->h_status[0] != 0) {
+        set_error(m->h_status[0], "llama_step: device packing rejected the descriptor (%d)", m->h_status[0]);
+        return m->h_status[0];
+    }
+    if (out_logits) memcpy(out_logits, m->h_logits, sizeof(float) * (size_t)n * c.vocab);
+    if (out_next) memcpy(out_next, m->h_next, sizeof(int32_t) * n);
+    for (int i = 0; i < n; ++i) sessions[i]->pos += n_new[i];
+    return 0;
+}
+
+int slate_hip_llama_batch_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessions, int n,
+                               const int32_t* tokens, float* out_logits) {
+    if (!m || n < 1 || n > m->max_slots) return -1;
+    std::vector<int32_t> ones(n, 1);
+    return slate_hip_llama_step(m, sessions, n, ones.data(), tokens, out_logits, nullptr);
+}
+
+int slate_hip_llama_prefill(slate_hip_llama_session_t* s, const int32_t* tokens, int n_tokens, float* out_logits) {
+    if (!s || !tokens || !out_logits || n_tokens <= 0) return -1;
+    slate_hip_llama* m = s->m;
+    if ((int64_t)s->pos + n_tokens > m->cfg.max_seq) return -2;
+    for (int i = 0; i < n_tokens; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab) return -3;
+    int done = 0;
+    while (done < n_tokens) {
+        int chunk = std::min(n_tokens - done, m->max_tokens);
+        bool last = done + chunk == n_tokens;
+        int rc = slate_hip_llama_step(m, &s, 1, &chunk, tokens + done, last ? out_logits : nullptr, nullptr);
+        if (rc) return rc;
+        done += chunk;
+    }
+    return 0;
+}
+
+int slate_hip_llama_decode_step(slate_hip_llama_session_t* s, int32_t token, float* out_logits) {
+    if (!s || !out_logits) return -1;
+    int one = 1;
+    return slate_hip_llama_step(s->m, &s, 1, &one, &token, out_logits, nullptr);
+}
+
+int slate_hip_llama_session_kv(const slate_hip_llama_session_t* s, float* K, float* V) {
+    if (!s || !K || !V) return -1;
+    slate_hip_llama* m = s->m;
+    const auto& c = m->cfg;
+    const int kvd = c.n_kv_heads * c.head_dim;
+    std::vector<float> buf((size_t)m->slot_stride);
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    if (hipStreamSynchronize(stream()) != hipSuccess) return -7;
+    for (int which = 0; which < 2; ++which) {
+        const float* src = (which ? m->Vpool : m->Kpool) + (int64_t)s->slot * m->slot_stride;
+        if (hipMemcpy(buf.data(), src, buf.size() * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) return -7;
+        float* dst = which ? V : K;
+        for (int li = 0; li < c.n_layers; ++li)
+            for (int h = 0; h < c.n_kv_heads; ++h)
+                for (int p = 0; p < c.max_seq; ++p)
+                    memcpy(dst + ((size_t)li * c.max_seq + p) * kvd + h * c.head_dim,
+                           buf.data() + li * m->layer_stride + h * m->head_stride + (int64_t)p * c.head_dim,
+                           sizeof(float) * c.head_dim);
+    }
+    return 0;
+}
+
+}  // extern "C"

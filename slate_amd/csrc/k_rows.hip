@@ -1,0 +1,368 @@
+// k_rows.hip -- row-wise kernels: RMSNorm (+residual), SiLU*mul, RoPE with
+// KV append, embedding gather, greedy argmax, ragged-batch packing and the
+// small f32 matmuls behind the vtable's matvec / linear_batch.
+#include "launch.h"
+
+namespace slate_hip {
+
+// Block-wide sum over 256 threads (wave64 shuffles, then LDS across waves).
+__device__ __forceinline__ double block_sum_256(double v, double* sh) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    double r = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r += sh[i];
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm of B rows (backend_cpu.c:48-76): inv = 1/sqrtf((float)(sum x^2 / D) + eps),
+// y = (x * w) * inv.  If delta != nullptr, x += sum_{s<nsplit} delta[s] first
+// (residual add of a split-K matmul result) and x is written back.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(float* __restrict__ y, float* __restrict__ x,
+                                                           const float* __restrict__ delta, int nsplit,
+                                                           int64_t split_stride, const float* __restrict__ w,
+                                                           int D, float eps) {
+#pragma clang fp contract(off)
+    __shared__ double sh[4];
+    const int r = blockIdx.x;
+    float* xr = x + (size_t)r * D;
+    float acc = 0.f;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float v = xr[d];
+        if (delta) {
+            const float* dr = delta + (size_t)r * D + d;
+            float s = dr[0];
+            for (int k = 1; k < nsplit; ++k) s += dr[(int64_t)k * split_stride];
+            v += s;
+            xr[d] = v;
+        }
+        acc = __builtin_fmaf(v, v, acc);
+    }
+    double sq = block_sum_256((double)acc, sh);
+    float inv = 1.0f / sqrtf((float)(sq / (double)D) + eps);
+    float* yr = y + (size_t)r * D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) yr[d] = (xr[d] * w[d]) * inv;
+}
+
+int launch_rmsnorm_rows(float* y, float* x, const float* delta, int nsplit, int64_t split_stride,
+                        const float* w, int B, int D, float eps, hipStream_t s) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(B), dim3(256), 0, s, y, x, delta, nsplit,
+                       split_stride, w, D, eps);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// y = silu(g) * u (backend_cpu.c:78-97).  gate/up may be split-K partials:
+// g = sum_s gate[s], u = sum_s up[s].
+__global__ void silu_mul_kernel(float* __restrict__ y, const float* __restrict__ gate,
+                                const float* __restrict__ up, int64_t n, int nsplit,
+                                int64_t split_stride, int H, int64_t gate_ld, int64_t up_ld) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t r = i / H, c = i - r * H;
+    const float* gp = gate + r * gate_ld + c;
+    const float* upp = up + r * up_ld + c;
+    float g = gp[0], u = upp[0];
+    for (int k = 1; k < nsplit; ++k) {
+        g += gp[(int64_t)k * split_stride];
+        u += upp[(int64_t)k * split_stride];
+    }
+    y[i] = (g / (1.0f + expf(-g))) * u;
+}
+
+int launch_silu_mul(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
+                    int64_t split_stride, int64_t gate_ld, int64_t up_ld, hipStream_t s) {
+    int64_t n = (int64_t)rows * H;
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, gate, up,
+                       n, nsplit, split_stride, H, gate_ld, up_ld);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+__global__ void add_kernel(float* __restrict__ y, const float* __restrict__ x, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] += x[i];
+}
+
+int launch_add(float* y, const float* x, int64_t n, hipStream_t s) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, x, n);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Embedding gather: y[t, :] = W[tok[t], :].  Tokens are validated on the
+// host; out-of-range ids are clamped here only to keep every access in bounds.
+__global__ void embed_rows_kernel(float* __restrict__ y, const float* __restrict__ W,
+                                  const int32_t* __restrict__ tok, int V, int D) {
+    int t = blockIdx.y;
+    int id = tok[t];
+    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+    for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < D; d += gridDim.x * blockDim.x)
+        y[(size_t)t * D + d] = W[(size_t)id * D + d];
+}
+
+int launch_embed_rows(float* y, const float* W, const int32_t* tok, int T, int V, int D, hipStream_t s) {
+    if (T <= 0) return 0;
+    dim3 grid((D + 255) / 256, T);
+    hipLaunchKernelGGL(embed_rows_kernel, grid, dim3(256), 0, s, y, W, tok, V, D);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// RoPE (llama_infer.c:77-92) from a host-built table: cs[(|p|*half + i)*2] =
+// {cosf(angle), sinf(angle)} with the reference's exact float expressions, so
+// rotation of identical inputs is bit-identical.  Negative positions use
+// cos(-a) = cos(a), sin(-a) = -sin(a).  Rows whose |pos| >= max_pos are left
+// unchanged and counted in *bad.
+__device__ __forceinline__ void rope_apply(float* x, int n_heads, int hd, int pos,
+                                           const float* __restrict__ cs, int lane, int nlanes) {
+#pragma clang fp contract(off)
+    int half = hd / 2;
+    int ap = pos < 0 ? -pos : pos;
+    float sg = pos < 0 ? -1.0f : 1.0f;
+    for (int idx = lane; idx < n_heads * half; idx += nlanes) {
+        int h = idx / half, i = idx - h * half;
+        float c = cs[((size_t)ap * half + i) * 2 + 0];
+        float s = sg * cs[((size_t)ap * half + i) * 2 + 1];
+        float* hh = x + h * hd;
+        float a = hh[i], b = hh[i + half];
+        hh[i] = a * c - b * s;
+        hh[i + half] = a * s + b * c;
+    }
+}
+
+__global__ void rope_rows_kernel(float* __restrict__ x, const int32_t* __restrict__ pos, int n_heads,
+                                 int hd, const float* __restrict__ cs, int max_pos, int* bad) {
+    int r = blockIdx.x;
+    int p = pos[r];
+    int ap = p < 0 ? -p : p;
+    if (ap >= max_pos) {
+        if (threadIdx.x == 0) atomicAdd(bad, 1);
+        return;
+    }
+    rope_apply(x + (size_t)r * n_heads * hd, n_heads, hd, p, cs, threadIdx.x, blockDim.x);
+}
+
+int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int hd, const float* cs,
+                     int max_pos, int* bad, hipStream_t s) {
+    if (n_rows <= 0) return 0;
+    hipLaunchKernelGGL(rope_rows_kernel, dim3(n_rows), dim3(256), 0, s, x, pos, n_heads, hd, cs, max_pos,
+                       bad);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// Fused epilogue of the QKV projection for a ragged step: sums split-K
+// partials of [T, D + 2*kv_dim], rotates q and k at each token's position,
+// writes q to qout and appends k, v into the sequence's KV cache
+// (pool layout [slot][layer][kv_head][max_seq][hd]).
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(
+    float* __restrict__ qout, float* __restrict__ Kpool, float* __restrict__ Vpool,
+    const float* __restrict__ part, int nsplit, int64_t split_stride, int qkv_ld,
+    const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
+    const int64_t* __restrict__ kv_base, int n_heads, int n_kv_heads, int hd, int64_t head_stride,
+    const float* __restrict__ cs) {
+    extern __shared__ float row[];      // D + 2*kv_dim floats
+    const int t = blockIdx.x;
+    const int D = n_heads * hd, kvd = n_kv_heads * hd;
+    const float* pr = part + (size_t)t * qkv_ld;
+    for (int c = threadIdx.x; c < D + 2 * kvd; c += blockDim.x) {
+        float v = pr[c];
+        for (int k = 1; k < nsplit; ++k) v += pr[(int64_t)k * split_stride + c];
+        row[c] = v;
+    }
+    __syncthreads();
+    const int p = tok_pos[t];
+    rope_apply(row, n_heads, hd, p, cs, threadIdx.x, blockDim.x);
+    rope_apply(row + D, n_kv_heads, hd, p, cs, threadIdx.x, blockDim.x);
+    __syncthreads();
+    for (int c = threadIdx.x; c < D; c += blockDim.x) qout[(size_t)t * D + c] = row[c];
+    const int64_t base = kv_base[tok2seq[t]];
+    for (int c = threadIdx.x; c < kvd; c += blockDim.x) {
+        int h = c / hd, d = c - h * hd;
+        int64_t off = base + (int64_t)h * head_stride + (int64_t)p * hd + d;
+        Kpool[off] = row[D + c];
+        Vpool[off] = row[D + kvd + c];
+    }
+}
+
+int launch_rope_kv_append(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit,
+                          int64_t split_stride, int qkv_ld, const int32_t* tok2seq,
+                          const int32_t* tok_pos, const int64_t* kv_base, int T, int n_heads,
+                          int n_kv_heads, int hd, int64_t head_stride, const float* cs, hipStream_t s) {
+    if (T <= 0) return 0;
+    size_t shm = (size_t)(n_heads + 2 * n_kv_heads) * hd * sizeof(float);
+    hipLaunchKernelGGL(rope_kv_append_kernel, dim3(T), dim3(256), shm, s, qout, Kpool, Vpool, part,
+                       nsplit, split_stride, qkv_ld, tok2seq, tok_pos, kv_base, n_heads, n_kv_heads, hd,
+                       head_stride, cs);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax per row with sampling.c:14-18 semantics: the first maximal
+// element wins (strict '>'), NaN is never selected unless element 0 is NaN,
+// in which case nothing compares greater and index 0 is returned.
+__global__ __launch_bounds__(256) void argmax_rows_kernel(int32_t* __restrict__ out,
+                                                          const float* __restrict__ logits, int V) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    const float* p = logits + (size_t)blockIdx.x * V;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int i = threadIdx.x; i < V; i += 256) {
+        float v = p[i];
+        if (v > bv || (bi < 0 && !(v != v))) { bv = v; bi = i; }
+    }
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            float v2 = sv[threadIdx.x + o];
+            int i2 = si[threadIdx.x + o];
+            float v1 = sv[threadIdx.x];
+            int i1 = si[threadIdx.x];
+            bool take = i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1));
+            if (take) { sv[threadIdx.x] = v2; si[threadIdx.x] = i2; }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        float p0 = p[0];
+        out[blockIdx.x] = (p0 != p0 || si[0] < 0) ? 0 : si[0];
+    }
+}
+
+int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, hipStream_t s) {
+    if (B <= 0) return 0;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(256), 0, s, out, logits, V);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Ragged-batch packing: one workgroup scans n_new (B <= 1024) and writes the
+// per-token indices.  status[0] = 0 ok, -1 bad descriptor, -2 over capacity.
+__global__ __launch_bounds__(1024) void pack_batch_kernel(
+    const int32_t* __restrict__ slot, const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_new,
+    int B, int max_seq, int64_t slot_stride, int T_cap, int32_t* __restrict__ tok_off,
+    int32_t* __restrict__ tok2seq, int32_t* __restrict__ tok_pos, int64_t* __restrict__ kv_base,
+    int32_t* __restrict__ last_tok, int32_t* __restrict__ status) {
+    __shared__ int32_t scan[1024];
+    __shared__ int32_t err;
+    const int b = threadIdx.x;
+    if (b == 0) err = 0;
+    __syncthreads();
+    int n = 0;
+    if (b < B) {
+        n = n_new[b];
+        int p0 = pos0[b];
+        if (n < 1 || p0 < 0 || slot[b] < 0) atomicMin(&err, -1);
+        else if ((int64_t)p0 + n > max_seq) atomicMin(&err, -2);
+    }
+    scan[b] = b < B ? n : 0;
+    __syncthreads();
+    // Hillis-Steele inclusive scan
+    for (int o = 1; o < 1024; o <<= 1) {
+        int32_t v = b >= o ? scan[b - o] : 0;
+        __syncthreads();
+        scan[b] += v;
+        __syncthreads();
+    }
+    int32_t total = scan[1023];
+    if (b == 0 && err == 0 && total > T_cap) err = -2;
+    __syncthreads();
+    if (b == 0) status[0] = err;
+    if (err != 0) return;
+    if (b < B) {
+        int32_t end = scan[b], start = end - n;
+        tok_off[b] = start;
+        if (b == B - 1) tok_off[B] = end;
+        kv_base[b] = (int64_t)slot[b] * slot_stride;
+        last_tok[b] = end - 1;
+        int p0 = pos0[b];
+        for (int i = 0; i < n; ++i) {
+            tok2seq[start + i] = b;
+            tok_pos[start + i] = p0 + i;
+        }
+    }
+}
+
+int launch_pack_batch(const int32_t* slot, const int32_t* pos0, const int32_t* n_new, int B, int max_seq,
+                      int64_t slot_stride, int T_cap, int32_t* tok_off, int32_t* tok2seq,
+                      int32_t* tok_pos, int64_t* kv_base, int32_t* last_tok, int32_t* status,
+                      hipStream_t s) {
+    if (B < 1 || B > 1024) return -1;
+    hipLaunchKernelGGL(pack_batch_kernel, dim3(1), dim3(1024), 0, s, slot, pos0, n_new, B, max_seq,
+                       slot_stride, T_cap, tok_off, tok2seq, tok_pos, kv_base, last_tok, status);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// f32 weights.  Y[b, m] = sum_k X[b, k] * W[m, k]: one wave per output row m,
+// lanes stride K, wave reduction; every batch row reuses the loaded W row.
+template <int BT>
+__global__ __launch_bounds__(256) void mm_f32_kernel(float* __restrict__ Y, const float* __restrict__ X,
+                                                     const float* __restrict__ W, int B, int M, int K,
+                                                     int ldy) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (m >= M) return;
+    const float* w = W + (size_t)m * K;
+    for (int b0 = 0; b0 < B; b0 += BT) {
+        float acc[BT];
+#pragma unroll
+        for (int i = 0; i < BT; ++i) acc[i] = 0.f;
+        for (int k = lane; k < K; k += 64) {
+            float wv = w[k];
+#pragma unroll
+            for (int i = 0; i < BT; ++i)
+                if (b0 + i < B) acc[i] = __builtin_fmaf(wv, X[(size_t)(b0 + i) * K + k], acc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < BT; ++i) {
+            float v = acc[i];
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (lane == 0 && b0 + i < B) Y[(size_t)(b0 + i) * ldy + m] = v;
+        }
+    }
+}
+
+int launch_mm_f32(float* Y, const float* X, const float* W, int B, int M, int K, int ldy, hipStream_t s) {
+    if (B <= 0 || M <= 0) return 0;
+    hipLaunchKernelGGL(mm_f32_kernel<8>, dim3((M + 3) / 4), dim3(256), 0, s, Y, X, W, B, M, K, ldy);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// C[b, n] = sum_k X[b, k] * W[k, n] (W is [K, N] for linear_batch, backend.h:58-61).
+__global__ void linear_batch_kernel(float* __restrict__ C, const float* __restrict__ X,
+                                    const float* __restrict__ W, int B, int K, int N) {
+    int n = blockIdx.x * blockDim.x + threadIdx.x;
+    int b = blockIdx.y;
+    if (n >= N) return;
+    const float* x = X + (size_t)b * K;
+    float acc = 0.f;
+    for (int k = 0; k < K; ++k) acc = __builtin_fmaf(x[k], W[(size_t)k * N + n], acc);
+    C[(size_t)b * N + n] = acc;
+}
+
+int launch_linear_batch(float* C, const float* X, const float* W, int B, int K, int N, hipStream_t s) {
+    if (B <= 0 || N <= 0) return 0;
+    hipLaunchKernelGGL(linear_batch_kernel, dim3((N + 255) / 256, B), dim3(256), 0, s, C, X, W, B, K, N);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+}  // namespace slate_hip

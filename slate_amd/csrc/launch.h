@@ -1,0 +1,49 @@
+// launch.h -- kernel launchers shared between the kernel files, the vtable
+// and the engine.  Every launcher enqueues on the given stream and returns 0
+// or a negative code (having recorded the sticky error).
+#pragma once
+
+#include "common.h"
+
+namespace slate_hip {
+
+// k_rows.hip
+int launch_rmsnorm_rows(float* y, float* x, const float* delta, int nsplit, int64_t split_stride,
+                        const float* w, int B, int D, float eps, hipStream_t s);
+int launch_silu_mul(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
+                    int64_t split_stride, int64_t gate_ld, int64_t up_ld, hipStream_t s);
+int launch_add(float* y, const float* x, int64_t n, hipStream_t s);
+int launch_embed_rows(float* y, const float* W, const int32_t* tok, int T, int V, int D, hipStream_t s);
+int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int hd, const float* cs,
+                     int max_pos, int* bad, hipStream_t s);
+int launch_rope_kv_append(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit,
+                          int64_t split_stride, int qkv_ld, const int32_t* tok2seq,
+                          const int32_t* tok_pos, const int64_t* kv_base, int T, int n_heads,
+                          int n_kv_heads, int hd, int64_t head_stride, const float* cs, hipStream_t s);
+int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, hipStream_t s);
+int launch_pack_batch(const int32_t* slot, const int32_t* pos0, const int32_t* n_new, int B, int max_seq,
+                      int64_t slot_stride, int T_cap, int32_t* tok_off, int32_t* tok2seq,
+                      int32_t* tok_pos, int64_t* kv_base, int32_t* last_tok, int32_t* status,
+                      hipStream_t s);
+int launch_mm_f32(float* Y, const float* X, const float* W, int B, int M, int K, int ldy, hipStream_t s);
+int launch_linear_batch(float* C, const float* X, const float* W, int B, int K, int N, hipStream_t s);
+
+// k_attn.hip
+int attn_chunk_size();
+size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
+int launch_attention_ragged(float* out, const float* q, const float* Kp, const float* Vp,
+                            const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
+                            int Hq, int Hkv, int HD, int64_t head_stride, int max_pos, float* po,
+                            float* pml, hipStream_t s);
+int launch_attention_step(float* out, const float* q, const float* K, const float* V, float* scores, int L,
+                          int D, hipStream_t s);
+
+// k_synth.hip
+int launch_synth_f32(float* dst, int64_t n, uint64_t seed, float std, float fill, hipStream_t s);
+int launch_synth_q4k(void* dst, int64_t rows, int64_t cols, uint64_t seed, float std, hipStream_t s);
+
+// Host-side RoPE table exactly as llama_infer.c:77-92 computes the angles:
+// cs[(p*half + i)*2 + {0,1}] = {cosf, sinf}(p * powf(theta, -2i/hd)).
+void build_rope_table(float* cs, int max_pos, int hd, float theta);
+
+}  // namespace slate_hip

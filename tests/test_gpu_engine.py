@@ -1,0 +1,179 @@
+"""The device LLaMA engine against slate's answers (golden.npz, produced by
+slate_llama_prefill / slate_llama_decode_step) and the oracle.
+
+Parity contract: logits within normwise relative 1e-3 of the reference f32
+CPU path; greedy token streams identical except where the reference's top-2
+logit gap is below that tolerance (then the rest of that stream is free to
+diverge and is not compared).
+"""
+import numpy as np
+import pytest
+
+import slate_amd
+from oracle.pyoracle import OracleModel
+from slate_amd.synth import LlamaShape, make_llama
+from tests.helpers import (N_GEN, Q4, Q4_PROMPT, Q4_SEED, TINY, TINY_SEED, relerr, tensors_digest,
+                           tiny_prompts)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def gap_ok(ref_logits):
+    """True when the reference's top-2 gap clears the tolerance."""
+    s = np.sort(ref_logits.astype(np.float64))
+    return (s[-1] - s[-2]) > TOL * max(np.abs(ref_logits).max(), 1e-30)
+
+
+def tiny_model(golden):
+    t = make_llama(TINY, TINY_SEED, quant="f32")
+    assert tensors_digest(t) == str(golden["tiny_digest"])
+    return t
+
+
+def test_tiny_llama_ragged_batch_matches_reference(golden):
+    """Config 1: 4 sequences prefilled, then decoded together as one ragged
+    batch for 32 steps (every step a batch of 4 different positions)."""
+    t = tiny_model(golden)
+    m = slate_amd.Llama.from_tensors(TINY, t, max_slots=4, max_tokens=64)
+    prompts = tiny_prompts()
+    sess = [m.session() for _ in prompts]
+    last = []
+    for s, p in zip(sess, prompts):
+        rc, lg = s.prefill(p)
+        assert rc == 0
+        last.append(lg)
+    alive = [True] * len(sess)
+    cur = np.stack(last)
+    for k in range(N_GEN):
+        ref = golden["tiny_logits"][:, k]
+        for i in range(len(sess)):
+            if alive[i]:
+                assert relerr(cur[i], ref[i]) < TOL, (i, k)
+        toks = []
+        for i in range(len(sess)):
+            tok = int(np.argmax(cur[i]))
+            if alive[i]:
+                if tok != golden["tiny_streams"][i, k]:
+                    assert not gap_ok(ref[i]), f"stream {i} diverged at step {k} with a clear top-2 gap"
+                    alive[i] = False
+            toks.append(tok)
+        rc, cur, nxt = m.step(sess, [1] * len(sess), toks)
+        assert rc == 0
+        assert list(nxt) == [int(np.argmax(c)) for c in cur]
+    assert all(alive), "every stream should match the reference for this workload"
+    for s, p in zip(sess, prompts):
+        assert s.position == len(p) + N_GEN
+
+
+def test_q4k_llama_matches_reference(golden):
+    t = make_llama(Q4, Q4_SEED, quant="q4k", output_quant="f32")
+    assert tensors_digest(t) == str(golden["q4_digest"])
+    m = slate_amd.Llama.from_tensors(Q4, t, max_slots=2, max_tokens=32)
+    s = m.session()
+    rc, lg = s.prefill(Q4_PROMPT)
+    assert rc == 0
+    for k in range(8):
+        assert relerr(lg, golden["q4_logits"][k]) < TOL, k
+        tok = int(np.argmax(lg))
+        assert tok == golden["q4_stream"][k] or not gap_ok(golden["q4_logits"][k])
+        rc, lg = s.decode(int(golden["q4_stream"][k]))
+        assert rc == 0
+    assert relerr(lg, golden["q4_logits"][8]) < TOL
+
+
+def test_batched_equals_sequential(golden):
+    """slate's test_infer.c:159-212 property for the LLaMA engine: one batched
+    step equals separate single-session steps (Linf < 1e-4)."""
+    t = tiny_model(golden)
+    m = slate_amd.Llama.from_tensors(TINY, t, max_slots=8, max_tokens=64)
+    prompts = [np.array(p[:6]) for p in tiny_prompts()]
+    nxt = [22, 13, 8, 27]
+    seq = []
+    for p, tk in zip(prompts, nxt):
+        s = m.session()
+        s.prefill(p)
+        seq.append(s.decode(tk)[1])
+        s.free()
+    sess = [m.session() for _ in prompts]
+    for s, p in zip(sess, prompts):
+        s.prefill(p)
+    rc, lg, _ = m.step(sess, [1] * 4, nxt)
+    assert rc == 0
+    assert np.max(np.abs(lg - np.stack(seq))) < 1e-4
+
+
+def test_mixed_prefill_and_decode_step(orc, golden):
+    """One ragged step carrying prompt chunks and single decode tokens at
+    once matches the oracle's token-serial processing; KV caches match."""
+    t = tiny_model(golden)
+    om = OracleModel(orc, TINY, t)
+    m = slate_amd.Llama.from_tensors(TINY, t, max_slots=4, max_tokens=64)
+    rng = np.random.default_rng(3)
+    first = [rng.integers(0, TINY.vocab, n).astype(np.int32) for n in (3, 7, 1, 12)]
+    second = [rng.integers(0, TINY.vocab, n).astype(np.int32) for n in (1, 5, 1, 9)]
+    sess = [m.session() for _ in first]
+    osess = [om.session() for _ in first]
+    rc, _, _ = m.step(sess, [len(a) for a in first], np.concatenate(first), want_logits=False)
+    assert rc == 0
+    rc, lg, nxt = m.step(sess, [len(a) for a in second], np.concatenate(second))
+    assert rc == 0
+    for i, (o, a, b) in enumerate(zip(osess, first, second)):
+        o.prefill(a)
+        _, want = o.prefill(b)
+        assert relerr(lg[i], want) < TOL
+        assert sess[i].position == len(a) + len(b) == o.position
+        K, V = sess[i].kv()
+        Ko, Vo = o.kv()
+        n = o.position
+        assert relerr(K[:, :n], Ko[:, :n]) < 1e-4 and relerr(V[:, :n], Vo[:, :n]) < 1e-4
+
+
+def test_engine_error_codes(golden):
+    """llama_infer.c:144-145 codes; a rejected step advances no session."""
+    shape = LlamaShape(**{**TINY.__dict__, "max_seq": 8})
+    t = make_llama(shape, 5, quant="f32")
+    m = slate_amd.Llama.from_tensors(shape, t, max_slots=2, max_tokens=16)
+    a, b = m.session(), m.session()
+    with pytest.raises(slate_amd.HipError):
+        m.session()                                  # both KV slots taken
+    slate_amd.load_library().slate_hip_clear_error()
+    assert a.decode(shape.vocab)[0] == -3
+    assert a.decode(-1)[0] == -3
+    assert m.step([a, b], [1, 1], [1, 999])[0] == -3
+    assert m.step([a, a], [1, 1], [1, 2])[0] == -1
+    assert m.step([a, b], [0, 1], [1])[0] == -1
+    assert a.position == 0 and b.position == 0
+    assert a.prefill(np.arange(8, dtype=np.int32))[0] == 0
+    assert a.decode(1)[0] == -2
+    assert m.step([a, b], [1, 1], [1, 2])[0] == -2
+    assert a.position == 8 and b.position == 0
+    assert m.step([b], [9], np.zeros(9, np.int32))[0] == -2
+    assert b.prefill(np.arange(17, dtype=np.int32) % 8)[0] == -2
+    a.free()
+    c = m.session()
+    assert c.position == 0
+
+
+def test_synthetic_q4k_engine_runs_and_is_batch_invariant():
+    """A device-generated Q4_K model (8B layer shapes, 2 layers, small vocab):
+    batched greedy decode equals one-at-a-time decode."""
+    shape = LlamaShape(n_layers=2, d_model=4096, n_heads=32, n_kv_heads=8, ffn=14336, vocab=4096,
+                       max_seq=512)
+    m = slate_amd.Llama.synthetic(shape, seed=7, quant=18, max_slots=5, max_tokens=64)
+    rng = np.random.default_rng(0)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (5, 17, 40, 2)]
+    sess = [m.session() for _ in prompts]
+    rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+    assert rc == 0 and np.all(np.isfinite(lg))
+    solo = m.session()
+    rc, lg1 = solo.prefill(prompts[2])
+    assert rc == 0
+    assert relerr(lg1, lg[2]) < 1e-5
+    toks = list(nxt)
+    for _ in range(4):
+        rc, lg, nxt = m.step(sess, [1] * 4, toks)
+        rc2, l2 = solo.decode(toks[2])
+        assert rc == 0 and rc2 == 0
+        assert relerr(l2, lg[2]) < 1e-5
+        toks = list(nxt)

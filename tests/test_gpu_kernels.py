@@ -1,0 +1,309 @@
+"""HIP kernels against the oracle and slate's golden answers, through the C ABI.
+
+Tolerances (from slate's own tests and the parity contract):
+* dequantised weights, RoPE rotation of identical inputs, argmax and packing
+  indices: bit-exact;
+* Q4_K matmul: normwise relative 1e-5 against the oracle's
+  slate_q4_k_matvec arithmetic, and per element 1e-4 relative to float64;
+* vtable row primitives: slate's test_backend.c Linf bounds (1e-4 matvec /
+  linear_batch, 1e-5 rmsnorm / silu / attention, exact add / embed / copy).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle.pyoracle import fp
+from slate_amd import DeviceBuffer as DB
+from slate_amd import check, load_library
+from slate_amd.synth import quantize_q4k
+from tests.helpers import bits, relerr, same_floats
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return DB.from_array(np.ascontiguousarray(a))
+
+
+def host(b, dtype, shape):
+    return b.to_array(dtype, shape)
+
+
+def tame_random_blocks(rng, nblocks):
+    """Random Q4_K bytes with finite, moderate d/dmin."""
+    b = rng.integers(0, 256, (nblocks, 144), dtype=np.uint8)
+    b[:, 1] = (b[:, 1] & 0x1F) | 0x10
+    b[:, 3] = (b[:, 3] & 0x1F) | 0x10
+    return np.ascontiguousarray(b.reshape(-1))
+
+
+# ------------------------------------------------------------ Q4_K
+def test_dequant_bitexact_golden(hip, golden):
+    raw = golden["q4k_raw"]
+    n = raw.size // 144 * 256
+    out = DB(n * 4)
+    check(hip.dequant_q4k(out.p, dev(raw).p, n), "dequant")
+    got = host(out, np.float32, n)
+    assert np.array_equal(bits(got), bits(golden["q4k_deq"]))
+
+
+def test_dequant_bitexact_random(hip, orc):
+    rng = np.random.default_rng(1)
+    raw = tame_random_blocks(rng, 4096 * 4)          # 4096 x 1024 weights
+    n = 4096 * 1024
+    out = DB(n * 4)
+    check(hip.dequant_q4k(out.p, dev(raw).p, n), "dequant")
+    got = host(out, np.float32, n)
+    assert np.array_equal(bits(got), bits(orc.dequant_q4k(raw, n)))
+    # every f16 header value: d and dmin sweep all 65536 bit patterns
+    blocks = np.zeros((65536, 144), np.uint8)
+    blocks[:, 0:2] = np.arange(65536, dtype=np.uint16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:4] = np.arange(65536, dtype=np.uint16)[::-1].copy().view(np.uint8).reshape(-1, 2)
+    blocks[:, 4:16] = rng.integers(0, 256, (65536, 12), dtype=np.uint8)
+    blocks[:, 16:] = rng.integers(0, 256, (65536, 128), dtype=np.uint8)
+    raw = np.ascontiguousarray(blocks.reshape(-1))
+    n = 65536 * 256
+    out = DB(n * 4)
+    check(hip.dequant_q4k(out.p, dev(raw).p, n), "dequant")
+    got = host(out, np.float32, n)
+    assert same_floats(got, orc.dequant_q4k(raw, n))
+
+
+@pytest.mark.parametrize("M,K", [(256, 256), (4096, 4096), (1024, 14336)])
+@pytest.mark.parametrize("B", [1, 3, 16, 17, 64, 70])
+def test_matmul_q4k(hip, orc, M, K, B):
+    if M * K > 4096 * 4096 and B > 17:
+        pytest.skip("oracle time budget")
+    rng = np.random.default_rng(M * 7 + K * 3 + B)
+    W = rng.normal(0, 0.02, (M, K)).astype(np.float32)
+    raw = np.frombuffer(quantize_q4k(W), np.uint8).copy()
+    X = rng.normal(0, 1, (B, K)).astype(np.float32)
+    Y = DB(B * M * 4)
+    check(hip.matmul_q4k(Y.p, dev(raw).p, dev(X).p, B, M, K), "matmul_q4k")
+    got = host(Y, np.float32, (B, M))
+    want = orc.q4k_matmul(raw, X, M, K)
+    assert relerr(got, want) < 1e-5
+    if M * K <= 4096 * 4096:
+        deq = orc.dequant_q4k(raw, M * K).reshape(M, K).astype(np.float64)
+        ref = X.astype(np.float64) @ deq.T
+        assert np.all(np.abs(got - ref) <= 1e-4 * np.abs(ref) + 1e-5 * np.abs(ref).max())
+
+
+def test_matmul_q4k_activation_scales(hip, orc):
+    """Rows spanning tiny to large magnitudes (the per-row power-of-two scale
+    keeps the f16 split accurate) and an all-zero row."""
+    rng = np.random.default_rng(4)
+    M, K = 512, 2048
+    raw = np.frombuffer(quantize_q4k(rng.normal(0, 0.02, (M, K)).astype(np.float32)), np.uint8).copy()
+    X = rng.normal(0, 1, (5, K)).astype(np.float32)
+    X[0] *= 1e-6
+    X[1] *= 3e3
+    X[2] = 0
+    X[3, ::7] *= 100.0
+    Y = DB(5 * M * 4)
+    check(hip.matmul_q4k(Y.p, dev(raw).p, dev(X).p, 5, M, K), "matmul_q4k")
+    got = host(Y, np.float32, (5, M))
+    want = orc.q4k_matmul(raw, X, M, K)
+    for r in (0, 1, 3, 4):
+        assert relerr(got[r], want[r]) < 1e-5, r
+    assert np.all(got[2] == 0)
+
+
+def test_matvec_q4k_vtable_golden(hip, golden):
+    M, K = golden["q4k_MK"]
+    raw = dev(golden["q4k_mv_raw"])
+    for i in range(3):
+        y = DB(M * 4)
+        hip.matvec_q4k(y.p, raw.p, dev(golden["q4k_x"][i]).p, M, K)
+        hip.sync()
+        check(0, "matvec_q4k")
+        assert relerr(host(y, np.float32, M), golden["q4k_y"][i]) < 1e-5
+
+
+# ------------------------------------------------------------ vtable KATs
+def test_vtable_known_answers(hip, golden):
+    """slate's tests/test_backend.c, staged through alloc/copy_h2d/copy_d2h."""
+    g = golden
+    assert hip.name == "hip"
+    # memory round trip, odd size
+    src = (np.arange(137, dtype=np.float32) * np.float32(0.5) - np.float32(12))
+    p = hip.alloc(137 * 4)
+    assert p
+    dst = np.empty_like(src)
+    hip.copy_h2d(p, src.ctypes.data, 137 * 4)
+    hip.copy_d2h(dst.ctypes.data, p, 137 * 4)
+    hip.release(p)
+    assert np.array_equal(dst, src)
+
+    y = DB(7 * 4)
+    hip.matvec(y.p, dev(g["kat_matvec_A"]).p, dev(g["kat_matvec_x"]).p, 7, 11)
+    assert np.max(np.abs(host(y, np.float32, 7) - g["kat_matvec_y"])) < 1e-4
+    Cb = DB(24 * 4)
+    hip.linear_batch(Cb.p, dev(g["kat_lb_X"]).p, dev(g["kat_lb_W"]).p, 4, 8, 6)
+    assert np.max(np.abs(host(Cb, np.float32, 24) - g["kat_lb_C"])) < 1e-4
+    yr = DB(16 * 4)
+    hip.rmsnorm_row(yr.p, dev(g["kat_rms_x"]).p, dev(g["kat_rms_w"]).p, 16, 1e-5)
+    assert np.max(np.abs(host(yr, np.float32, 16) - g["kat_rms_y"])) < 1e-5
+    gb = dev(g["kat_silu_g"])
+    hip.silu_mul(gb.p, gb.p, dev(g["kat_silu_u"]).p, 24)          # in place, as llama_infer.c:192
+    assert np.max(np.abs(host(gb, np.float32, 24) - g["kat_silu_y"])) < 1e-5
+    y0 = np.arange(32, dtype=np.float32) * np.float32(0.1)
+    x0 = (np.arange(32) - 16).astype(np.float32) * np.float32(0.2)
+    ya = dev(y0)
+    hip.add_inplace(ya.p, dev(x0).p, 32)
+    assert np.array_equal(host(ya, np.float32, 32), y0 + x0)
+    W = np.arange(40, dtype=np.float32)
+    ye = DB(8 * 4)
+    hip.embed_lookup(ye.p, dev(W).p, 3, 8)
+    assert np.array_equal(host(ye, np.float32, 8), W[24:32])
+    o = DB(16 * 4)
+    sc = DB(5 * 4)
+    hip.attention_step(o.p, dev(g["kat_att_q"]).p, dev(g["kat_att_K"]).p, dev(g["kat_att_V"]).p, sc.p, 5, 16)
+    assert np.max(np.abs(host(o, np.float32, 16) - g["kat_att_out"])) < 1e-5
+    L, D = g["att64_K"].shape
+    o = DB(D * 4)
+    sc = DB(L * 4)
+    hip.attention_step(o.p, dev(g["att64_q"]).p, dev(g["att64_K"]).p, dev(g["att64_V"]).p, sc.p, L, D)
+    assert np.max(np.abs(host(o, np.float32, D) - g["att64_out"])) < 1e-5
+    for Dn in (37, 4096):
+        yy = DB(Dn * 4)
+        hip.rmsnorm_row(yy.p, dev(g[f"rms{Dn}_x"]).p, dev(g[f"rms{Dn}_w"]).p, Dn, 1e-5)
+        assert np.max(np.abs(host(yy, np.float32, Dn) - g[f"rms{Dn}_y"])) < 1e-5
+        ss = DB(Dn * 4)
+        hip.silu_mul(ss.p, dev(g[f"silu{Dn}_g"]).p, dev(g[f"rms{Dn}_w"]).p, Dn)
+        assert np.max(np.abs(host(ss, np.float32, Dn) - g[f"silu{Dn}_y"])) < 1e-5
+    hip.sync()
+    check(0, "vtable")
+
+
+def test_matvec_linear_batch_random(hip, orc):
+    rng = np.random.default_rng(8)
+    for M, K in ((172, 64), (64, 172), (300, 1000)):
+        A = rng.normal(0, 0.5, (M, K)).astype(np.float32)
+        x = rng.normal(0, 1, K).astype(np.float32)
+        y = DB(M * 4)
+        hip.matvec(y.p, dev(A).p, dev(x).p, M, K)
+        want = np.empty(M, np.float32)
+        orc.lib.orc_matvec(fp(want), fp(A), fp(x), M, K)
+        assert np.max(np.abs(host(y, np.float32, M) - want)) < 1e-4
+        Bn, N = 5, M
+        X = rng.normal(0, 1, (Bn, K)).astype(np.float32)
+        W = rng.normal(0, 0.5, (K, N)).astype(np.float32)
+        Cd = DB(Bn * N * 4)
+        hip.linear_batch(Cd.p, dev(X).p, dev(W).p, Bn, K, N)
+        want = np.empty((Bn, N), np.float32)
+        orc.lib.orc_linear_batch(fp(want), fp(X), fp(W), Bn, K, N)
+        assert np.max(np.abs(host(Cd, np.float32, (Bn, N)) - want)) < 1e-4
+
+
+# ------------------------------------------------------------ RoPE
+def test_rope_rows_bitexact_golden(hip, golden):
+    x, y, pos = golden["rope_x"], golden["rope_y"], golden["rope_pos"]
+    xb = dev(x)
+    check(hip.rope_rows(xb.p, dev(pos).p, len(pos), 4, 128, 10000.0, 16384), "rope_rows")
+    assert np.array_equal(bits(host(xb, np.float32, x.shape)), bits(y))
+
+
+def test_rope_rows_rejects_out_of_range(hip):
+    xb = dev(np.ones((2, 64), np.float32))
+    rc = hip.rope_rows(xb.p, dev(np.array([3, 99], np.int32)).p, 2, 1, 64, 10000.0, 50)
+    assert rc == -1
+    load_library().slate_hip_clear_error()
+    # the in-range row was rotated, the other left as it was
+    out = host(xb, np.float32, (2, 64))
+    assert np.array_equal(out[1], np.ones(64, np.float32))
+
+
+# ------------------------------------------------------------ argmax / packing
+def test_argmax_rows(hip, orc):
+    rng = np.random.default_rng(12)
+    B, V = 16, 128256
+    L = rng.integers(-1000, 1000, (B, V)).astype(np.float32)   # many exact ties
+    L[3, :] = 7.0
+    L[4, 5] = np.nan
+    out = DB(B * 4)
+    check(hip.argmax_rows(out.p, dev(L).p, B, V), "argmax")
+    got = host(out, np.int32, B)
+    want = [orc.lib.orc_argmax(fp(np.ascontiguousarray(L[b])), V) for b in range(B)]
+    assert list(got) == want
+    L2 = np.full((2, 10), 1.0, np.float32)
+    L2[0, 0] = np.nan
+    out2 = DB(8)
+    check(hip.argmax_rows(out2.p, dev(L2).p, 2, 10), "argmax")
+    assert list(host(out2, np.int32, 2)) == [0, 0]
+
+
+def test_pack_batch_bitexact(orc):
+    lib = load_library()
+    rng = np.random.default_rng(21)
+    for trial in range(30):
+        B = int(rng.integers(1, 64))
+        slot = rng.permutation(128)[:B].astype(np.int32)
+        n_new = np.where(rng.random(B) < 0.6, 1, rng.integers(1, 64, B)).astype(np.int32)
+        pos0 = rng.integers(0, 2048, B).astype(np.int32)
+        if trial == 7:
+            n_new[3 % B] = 0
+        if trial == 8:
+            pos0[0] = 2300
+        stride, max_seq, cap = 75497472, 2304, 4096
+        rc, want = orc.pack_batch(slot, pos0, n_new, max_seq, stride)
+        T = max(int(n_new.sum()), 1)
+        outs = [DB((B + 1) * 4), DB(cap * 4), DB(cap * 4), DB(B * 8), DB(B * 4), DB(16)]
+        r = lib.slate_hip_pack_batch(dev(slot).p, dev(pos0).p, dev(n_new).p, B, max_seq, stride, cap,
+                                     *[o.p for o in outs])
+        check(r, "pack_batch")
+        status = host(outs[5], np.int32, 4)[0]
+        if rc < 0:
+            assert status == rc
+            continue
+        assert status == 0
+        got = dict(tok_off=host(outs[0], np.int32, B + 1), tok2seq=host(outs[1], np.int32, T),
+                   tok_pos=host(outs[2], np.int32, T), kv_base=host(outs[3], np.int64, B),
+                   last_tok=host(outs[4], np.int32, B))
+        for k in want:
+            assert np.array_equal(got[k], want[k][:len(got[k])]), k
+
+
+# ------------------------------------------------------------ attention
+@pytest.mark.parametrize("hd,Hq,Hkv", [(128, 32, 8), (16, 4, 2), (64, 8, 8)])
+def test_attention_ragged_vs_oracle(hip, orc, hd, Hq, Hkv):
+    """Per-token GQA attention over ragged per-sequence caches, one query per
+    token (decode) and several consecutive queries of one sequence (prefill
+    chunk), lengths across chunk boundaries."""
+    lib = load_library()
+    rng = np.random.default_rng(hd + Hq)
+    max_seq = 4352
+    lens = [1, 2, 255, 256, 257, 1000, 4097, 64]
+    nslot = len(lens)
+    head_stride = max_seq * hd
+    slot_stride = Hkv * head_stride
+    Kp = rng.normal(0, 1, nslot * slot_stride).astype(np.float32)
+    Vp = rng.normal(0, 1, nslot * slot_stride).astype(np.float32)
+    tok2seq, tok_pos = [], []
+    for b, L in enumerate(lens):
+        tok2seq.append(b)
+        tok_pos.append(L - 1)
+    tok2seq += [5, 5, 5]               # a prefill chunk: positions 10..12 of sequence 5
+    tok_pos += [10, 11, 12]
+    T = len(tok2seq)
+    kv_base = (np.arange(nslot, dtype=np.int64)[::-1] * slot_stride).copy()   # slot b -> nslot-1-b
+    q = rng.normal(0, 1, (T, Hq * hd)).astype(np.float32)
+    out = DB(T * Hq * hd * 4)
+    r = lib.slate_hip_attention_ragged(out.p, dev(q).p, dev(Kp).p, dev(Vp).p,
+                                       dev(np.array(tok2seq, np.int32)).p, dev(np.array(tok_pos, np.int32)).p,
+                                       dev(kv_base).p, T, Hq, Hkv, hd, head_stride, max_seq)
+    check(r, "attention_ragged")
+    got = host(out, np.float32, (T, Hq * hd))
+    Kp = Kp.reshape(nslot, Hkv, max_seq, hd)
+    Vp = Vp.reshape(nslot, Hkv, max_seq, hd)
+    for t in range(T):
+        s = nslot - 1 - tok2seq[t]
+        L = tok_pos[t] + 1
+        Kc = np.ascontiguousarray(Kp[s, :, :L].transpose(1, 0, 2).reshape(L, Hkv * hd))
+        Vc = np.ascontiguousarray(Vp[s, :, :L].transpose(1, 0, 2).reshape(L, Hkv * hd))
+        want = np.empty(Hq * hd, np.float32)
+        sc = np.empty(L, np.float32)
+        orc.lib.orc_attention_multihead(fp(want), fp(np.ascontiguousarray(q[t])), fp(Kc), fp(Vc), fp(sc),
+                                        L, Hq, Hkv, hd)
+        assert np.max(np.abs(got[t] - want)) < 1e-5, (t, L)
