@@ -144,6 +144,11 @@ def check(rc=0, what="call"):
         raise HipError(f"{what}: {msg} (rc={rc})")
 
 
+class DevicePtr(C.c_void_p):
+    """A device address that keeps its DeviceBuffer alive while it exists, so
+    `f(DeviceBuffer.from_array(a).p)` cannot free the memory before f runs."""
+
+
 class DeviceBuffer:
     """A device allocation made through the vtable's alloc()."""
 
@@ -186,7 +191,9 @@ class DeviceBuffer:
 
     @property
     def p(self):
-        return C.c_void_p(self.ptr)
+        v = DevicePtr(self.ptr)
+        v._owner = self
+        return v
 
 
 class Backend:
