@@ -1,0 +1,263 @@
+#!/usr/bin/env python3
+"""Benchmark: LLaMA-3-8B-shaped Q4_K decode under ragged continuous batching.
+
+Workload (one MI355X): 32 layers, d_model 4096, 32 Q / 8 KV heads, head_dim
+128, SwiGLU 14336, vocab 128256; every linear weight Q4_K drawn N(0, 0.02)
+on the device from a fixed seed, embeddings f32, norms 1.  B = 16 sequences;
+contexts prefilled to U[128, 2048] tokens (untimed); each sequence stops after
+U[32, 256] generated tokens and its slot is taken by a new arrival whose
+U[64, 512]-token prompt is prefilled inside the next ragged step (timed, mixed
+prefill + decode).  A step = one pass of the engine over the packed batch;
+each step produces one token per sequence.
+
+Printed: one JSON line.  value = generated tokens / wall time over K timed
+steps (weights and KV resident in HBM).  roofline = the dominant kernel class
+(Q4_K matmul or attention) by device time, from HIP events recorded on the
+backend stream around every launch in the timed steps: achieved = algorithmic
+bytes / device time.  cpu_baseline = slate's own C decode step
+(slate_llama_decode_step, single thread as wired) on the same weights and KV
+state, for one step of all 16 sequences.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s at B=16 ragged, 8B-shape Q4_K; Q4_K matmul HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """Continuous-batching driver over the engine's ragged step."""
+
+    def __init__(self, m, shape, B, seed, max_tokens):
+        self.m, self.shape, self.B = m, shape, B
+        self.rng = np.random.default_rng(seed)
+        self.max_tokens = max_tokens
+        self.sess = [None] * B
+        self.pending = [None] * B      # prompt still to prefill
+        self.last = [0] * B            # last generated token
+        self.gen = [0] * B
+        self.stop = [0] * B
+        self.arrivals = 0
+
+    def new_prompt(self, lo, hi):
+        n = int(self.rng.integers(lo, hi + 1))
+        return self.rng.integers(0, self.shape.vocab, n).astype(np.int32)
+
+    def start(self, i, prompt):
+        if self.sess[i] is not None:
+            self.sess[i].free()
+        self.sess[i] = self.m.session()
+        self.pending[i] = prompt
+        self.gen[i] = 0
+        self.stop[i] = int(self.rng.integers(32, 257))
+
+    def prefill_all(self):
+        """Untimed: initial contexts U[128, 2048], packed several per step."""
+        for i in range(self.B):
+            self.start(i, self.new_prompt(128, 2048))
+        todo = list(range(self.B))
+        while todo:
+            group, T = [], 0
+            for i in todo:
+                if T + len(self.pending[i]) <= self.max_tokens:
+                    group.append(i)
+                    T += len(self.pending[i])
+            todo = [i for i in todo if i not in group]
+            rc, _, nxt = self.m.step([self.sess[i] for i in group], [len(self.pending[i]) for i in group],
+                                     np.concatenate([self.pending[i] for i in group]), want_logits=False)
+            assert rc == 0, f"prefill step rc={rc}"
+            for i, t in zip(group, nxt):
+                self.pending[i] = None
+                self.last[i] = int(t)
+                self.gen[i] = 1
+
+    def step(self, want_logits=False):
+        n_new, toks = [], []
+        for i in range(self.B):
+            if self.pending[i] is not None:
+                n_new.append(len(self.pending[i]))
+                toks.append(self.pending[i])
+            else:
+                n_new.append(1)
+                toks.append(np.array([self.last[i]], np.int32))
+        mixed = any(n > 1 for n in n_new)
+        rc, lg, nxt = self.m.step(self.sess, n_new, np.concatenate(toks), want_logits=want_logits)
+        assert rc == 0, f"step rc={rc}"
+        for i in range(self.B):
+            self.pending[i] = None
+            self.last[i] = int(nxt[i])
+            self.gen[i] += 1
+            if self.gen[i] >= self.stop[i]:
+                self.arrivals += 1
+                self.start(i, self.new_prompt(64, 512))
+        return mixed, lg
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU sharding is described "
+                                   "in DESIGN.md and not executed", "n_gpus": args.gpus}))
+        return 2
+
+    import slate_amd
+    from slate_amd.synth import LlamaShape
+    shape = LlamaShape(n_layers=args.layers, d_model=4096, n_heads=32, n_kv_heads=8, ffn=14336,
+                       vocab=128256, max_seq=2304)
+    max_tokens = 4096
+    t0 = time.perf_counter()
+    m = slate_amd.Llama.synthetic(shape, seed=args.seed, quant=18, max_slots=args.batch + 1,
+                                  max_tokens=max_tokens)
+    log(f"synthetic 8B-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
+    wl = Workload(m, shape, args.batch, args.seed + 1, max_tokens)
+    t0 = time.perf_counter()
+    wl.prefill_all()
+    ctx0 = [s.position for s in wl.sess]
+    log(f"prefilled {sum(ctx0)} context tokens in {time.perf_counter() - t0:.1f} s")
+    for _ in range(args.warmup):
+        wl.step()
+    lib = slate_amd.load_library()
+    m.profile(True)
+    lib.slate_hip_sync()
+    arrivals0 = wl.arrivals
+    mixed_steps = 0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        mixed_steps += wl.step()[0]
+    lib.slate_hip_sync()
+    dt = time.perf_counter() - t0
+    prof = m.profile_read()
+    m.profile(False)
+    tokens = args.batch * args.steps
+    value = tokens / dt
+    log(f"{args.steps} steps in {dt:.3f} s, {mixed_steps} with arrivals ({wl.arrivals - arrivals0} arrivals)")
+    for k, (ms, by, n) in prof.items():
+        log(f"  {k:10s} {ms:9.2f} ms  {n:6d} launches  {by / max(ms, 1e-9) / 1e6:8.1f} GB/s")
+
+    # dominant kernel class by device time
+    dom = max(("q4k_mm", "attention"), key=lambda k: prof[k][0])
+    ms, by, n = prof[dom]
+    achieved = by / (ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "kernel": "q4k_mm_kernel" if dom == "q4k_mm" else "attn_chunk_kernel+attn_merge_kernel",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "launches": n, "avg_launch_us": round(ms * 1e3 / max(n, 1), 2),
+                "algorithmic_bytes_per_launch": round(by / max(n, 1))}
+    other = "attention" if dom == "q4k_mm" else "q4k_mm"
+    oms, oby, on = prof[other]
+    step_ms, _, step_n = prof["step"]
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "LLaMA-3-8B-shaped Q4_K decode, ragged continuous batching B=16 "
+                               "(contexts U[128,2048], stop U[32,256], arrivals with U[64,512]-token prompts)",
+                   "layers": args.layers, "d_model": 4096, "heads": "32q/8kv", "ffn": 14336, "vocab": 128256,
+                   "weights": "q4_k", "kv_cache": "f32", "batch": args.batch,
+                   "mixed_prefill_steps": mixed_steps, "arrivals": wl.arrivals - arrivals0,
+                   "mean_context_start": round(float(np.mean(ctx0)), 1)},
+        "roofline": roofline,
+        "kernels": {"other_class": other, f"{other}_GBs": round(oby / max(oms, 1e-9) / 1e6, 1),
+                    f"{other}_ms": round(oms, 2), "device_step_ms": round(step_ms / max(step_n, 1), 3)},
+    }
+    if not args.no_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline_and_parity(m, shape, wl)
+        except Exception as e:  # the baseline is reported, never required
+            result["cpu_baseline"] = {"error": str(e)}
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def cpu_baseline_and_parity(m, shape, wl):
+    """Snapshot KV of every decoding sequence, run the CPU reference step from
+    that state, then the GPU step; compare the two sets of logits."""
+    snap = [(i, wl.sess[i].kv(), wl.sess[i].position, wl.last[i]) for i in range(wl.B)
+            if wl.pending[i] is None]
+    _, lg, _ = wl.m.step([wl.sess[i] for i, *_ in snap], [1] * len(snap),
+                         [t for *_, t in snap], want_logits=True)
+    gpu = {i: lg[k] for k, (i, *_) in enumerate(snap)}
+    return cpu_baseline_from(m, shape, snap, gpu)
+
+
+def cpu_baseline_from(m, shape, snap, gpu, budget_s=40.0):
+    from oracle.pyoracle import Ref, RefLlama, ref_available
+    from slate_amd.gguf import GGML_F32, GGML_Q4_K, GGUFWriter
+    if not ref_available():
+        return {"error": "oracle/_ref not built"}
+    ref = Ref()
+    path = "/dev/shm/slate_amd_bench_8b.gguf"
+    g = GGUFWriter()
+    g.add_str("general.architecture", "llama")
+    for k, v in (("block_count", shape.n_layers), ("embedding_length", shape.d_model),
+                 ("feed_forward_length", shape.ffn), ("attention.head_count", shape.n_heads),
+                 ("attention.head_count_kv", shape.n_kv_heads), ("context_length", shape.max_seq),
+                 ("vocab_size", shape.vocab)):
+        g.add_u32("llama." + k, v)
+    g.add_f32("llama.rope.freq_base", shape.theta)
+    g.add_f32("llama.attention.layer_norm_rms_epsilon", shape.eps)
+    D, H, kv = shape.d_model, shape.ffn, shape.kv_dim
+    dims = {"attn_q": (D, D), "attn_k": (kv, D), "attn_v": (kv, D), "attn_output": (D, D),
+            "ffn_gate": (H, D), "ffn_up": (H, D), "ffn_down": (D, H)}
+
+    def add(name, gname, shp):
+        raw, dt = m.get_tensor(name)
+        g.add_tensor(gname, shp, GGML_Q4_K if dt == 18 else GGML_F32, raw)
+
+    add("token_embd", "token_embd.weight", (shape.vocab, D))
+    add("output_norm", "output_norm.weight", (D,))
+    add("output", "output.weight", (shape.vocab, D))
+    for i in range(shape.n_layers):
+        add(f"blk.{i}.attn_norm", f"blk.{i}.attn_norm.weight", (D,))
+        add(f"blk.{i}.ffn_norm", f"blk.{i}.ffn_norm.weight", (D,))
+        for n, shp in dims.items():
+            add(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", shp)
+    g.write(path)
+    del g
+    rm = RefLlama(ref, path)
+    t_cpu, n_tok, worst = 0.0, 0, 0.0
+    try:
+        for i, (K, V), pos, tok in snap:
+            rs = rm.session()
+            assert rs.set_state(K, V, pos) == 0
+            t0 = time.perf_counter()
+            rc, lg = rs.decode(tok)
+            t_cpu += time.perf_counter() - t0
+            rs.free()
+            assert rc == 0
+            n_tok += 1
+            worst = max(worst, float(np.abs(lg - gpu[i]).max() / max(np.abs(lg).max(), 1e-30)))
+            if t_cpu > budget_s:
+                break
+    finally:
+        rm.close()
+        os.unlink(path)
+    return dict(value=round(n_tok / t_cpu, 4), unit="tok/s", cores=1, kind="reference",
+                sample=f"slate_llama_decode_step (slate's C, built from its sources, single thread as wired) "
+                       f"on the benchmark's weights and KV state: one decode step of {n_tok} sequences, "
+                       f"{t_cpu:.1f} s",
+                host_cores_available=os.cpu_count(), logits_max_rel_vs_gpu=worst)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -208,6 +208,16 @@ int   slate_hip_llama_batch_step(slate_hip_llama_t* m, slate_hip_llama_session_t
  * reference session layout, llama_infer.c:57-58) for checking. */
 int   slate_hip_llama_session_kv(const slate_hip_llama_session_t* s, float* K, float* V);
 
+/* Kernel-class timing with HIP events recorded on the backend stream around
+ * each launch: class 0 = Q4_K matmuls, 1 = attention, 2 = whole steps.
+ * profile(m, 1) resets the totals and starts recording, profile(m, 0) stops.
+ * profile_read returns the summed device milliseconds, the summed
+ * algorithmic bytes (weights once, K/V once per kv head and sequence,
+ * activations in and out) and the launch count of a class. */
+int   slate_hip_llama_profile(slate_hip_llama_t* m, int enable);
+int   slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes,
+                                   int64_t* launches);
+
 /* The backend stream as a hipStream_t (for timing with events). */
 void* slate_hip_stream(void);
 

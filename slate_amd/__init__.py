@@ -99,6 +99,9 @@ SIGNATURES = {
     "slate_hip_llama_step": (C.c_int, [vp, vp, C.c_int, vp, vp, vp, vp]),
     "slate_hip_llama_batch_step": (C.c_int, [vp, vp, C.c_int, vp, vp]),
     "slate_hip_llama_session_kv": (C.c_int, [vp, vp, vp]),
+    "slate_hip_llama_profile": (C.c_int, [vp, C.c_int]),
+    "slate_hip_llama_profile_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double),
+                                               C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
 }
 
 _lib = None
@@ -313,6 +316,18 @@ class Llama:
 
     def session(self):
         return Session(self)
+
+    def profile(self, enable=True):
+        check(self.lib.slate_hip_llama_profile(self.h, 1 if enable else 0), "profile")
+
+    def profile_read(self):
+        """{class: (device ms, algorithmic bytes, launches)} for q4k, attention, step."""
+        out = {}
+        for cls, name in enumerate(("q4k_mm", "attention", "step")):
+            ms, by, n = C.c_double(), C.c_double(), C.c_int64()
+            self.lib.slate_hip_llama_profile_read(self.h, cls, C.byref(ms), C.byref(by), C.byref(n))
+            out[name] = (ms.value, by.value, n.value)
+        return out
 
     def step(self, sessions, n_new, tokens, want_logits=True):
         n = len(sessions)

@@ -125,7 +125,7 @@ void build_rope_table(float* cs, int max_pos, int hd, float theta) {
 // Activation buffers for one Q4_K matmul input of B rows x K.
 int make_act16(Act16& a, int B, int K, int slot) {
     a.rows = B;
-    a.rows_pad = (B + 15) / 16 * 16;
+    a.rows_pad = row_pad(B);
     a.K = K;
     size_t nx = (size_t)a.rows_pad * K;
     size_t ny = (size_t)a.rows_pad * (K / 32) * 2;

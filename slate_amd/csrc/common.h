@@ -69,6 +69,9 @@ int launch_q4k_mm(const void* W, const Act16& a, float* out, int64_t ldo, int64_
 int launch_sum_splits(float* Y, const float* part, int nsplit, int rows, int rows_pad, int M,
                       hipStream_t s);
 int q4k_pick_splits(int M, int K, int rows_pad);
+// Activation rows are padded to whole 16-row MFMA tiles, and to whole groups
+// of four tiles beyond 64 rows, so every launch uses a single tile count.
+inline int row_pad(int rows) { return rows <= 64 ? (rows + 15) / 16 * 16 : (rows + 63) / 64 * 64; }
 // Carve an Act16 for B rows x K out of backend scratch slot `slot`.
 int make_act16(Act16& a, int B, int K, int slot);
 

@@ -67,11 +67,24 @@ struct slate_hip_llama {
     int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
             *last_tok = nullptr, *status = nullptr, *next = nullptr;
     int64_t* kv_base = nullptr;
+    // Per-step host input, uploaded in one copy: [slot|pos0|n_new (max_slots
+    // each)] [tokens (T)] [decode query blocks (n_dec)] [prefill block first
+    // tokens (n_pre)] [prefill block sizes (n_pre)]; d_desc mirrors it.
     int32_t *h_desc = nullptr, *h_tok = nullptr, *h_next = nullptr, *h_status = nullptr;
+    int n_dec = 0, n_pre = 0;
     float* h_logits = nullptr;
     std::vector<int> free_slots;
     std::vector<void*> allocs;
     std::mutex mu;
+    // Optional event timing of kernel classes (slate_hip_llama_profile).
+    struct ProfRec { int cls; double bytes; size_t e0, e1; };
+    bool prof_on = false;
+    std::vector<hipEvent_t> prof_ev;
+    size_t prof_used = 0;
+    std::vector<ProfRec> prof_recs;
+    double prof_ms[3] = {0, 0, 0}, prof_bytes[3] = {0, 0, 0};
+    int64_t prof_n[3] = {0, 0, 0};
+    double step_kv_rows = 0;     // sum over sequences of positions attended this step
 };
 
 struct slate_hip_llama_session {
@@ -101,7 +114,6 @@ void free_model(slate_hip_llama* m) {
     (void)hipStreamSynchronize(stream());
     for (void* p : m->allocs) (void)hipFree(p);
     if (m->h_desc) (void)hipHostFree(m->h_desc);
-    if (m->h_tok) (void)hipHostFree(m->h_tok);
     if (m->h_next) (void)hipHostFree(m->h_next);
     if (m->h_status) (void)hipHostFree(m->h_status);
     if (m->h_logits) (void)hipHostFree(m->h_logits);
@@ -118,7 +130,7 @@ bool valid_cfg(const slate_hip_llama_config_t* c) {
 int alloc_runtime(slate_hip_llama* m) {
     const auto& c = m->cfg;
     const int D = c.d_model, H = c.ffn_hidden, kvd = c.n_kv_heads * c.head_dim;
-    m->tpad_cap = (m->max_tokens + 15) / 16 * 16;
+    m->tpad_cap = row_pad(m->max_tokens);
     m->head_stride = (int64_t)c.max_seq * c.head_dim;
     m->layer_stride = (int64_t)c.n_kv_heads * m->head_stride;
     m->slot_stride = (int64_t)c.n_layers * m->layer_stride;
@@ -138,7 +150,7 @@ int alloc_runtime(slate_hip_llama* m) {
     if (dalloc(m, &m->x, T * D) || dalloc(m, &m->xn, T * D) || dalloc(m, &m->q, T * D) ||
         dalloc(m, &m->att, T * D) || dalloc(m, &m->h, T * H) || dalloc(m, &m->xlast, (size_t)m->max_slots * D) ||
         // the LM-head matmul writes whole 16-row tiles
-        dalloc(m, &m->logits, (size_t)((m->max_slots + 15) / 16 * 16) * c.vocab))
+        dalloc(m, &m->logits, (size_t)row_pad(m->max_slots) * c.vocab))
         return -2;
     const int W = std::max({D + 2 * kvd, 2 * H, D});
     m->part_floats = (size_t)std::max<size_t>(16 * 64, T) * W;
@@ -155,18 +167,26 @@ int alloc_runtime(slate_hip_llama* m) {
         dalloc(m, &a.rinv, T))
         return -2;
     const int S = m->max_slots;
-    if (dalloc(m, &m->d_desc, 3 * (size_t)S) || dalloc(m, &m->d_tok, T) || dalloc(m, &m->tok_off, S + 1) ||
+    const size_t in_ints = 3 * (size_t)S + 4 * T;
+    if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
         dalloc(m, &m->tok2seq, T) || dalloc(m, &m->tok_pos, T) || dalloc(m, &m->last_tok, S) ||
         dalloc(m, &m->status, 4) || dalloc(m, &m->next, S) || dalloc(m, &m->kv_base, S))
         return -2;
-    if (hipHostMalloc((void**)&m->h_desc, 3 * sizeof(int32_t) * S) != hipSuccess ||
-        hipHostMalloc((void**)&m->h_tok, sizeof(int32_t) * T) != hipSuccess ||
+    m->d_tok = m->d_desc + 3 * S;
+    // index buffers start as valid (all-zero) indices
+    if (hipMemset(m->tok2seq, 0, T * 4) != hipSuccess || hipMemset(m->tok_pos, 0, T * 4) != hipSuccess ||
+        hipMemset(m->kv_base, 0, S * 8) != hipSuccess || hipMemset(m->last_tok, 0, S * 4) != hipSuccess) {
+        set_error(-7, "engine: index clear failed");
+        return -7;
+    }
+    if (hipHostMalloc((void**)&m->h_desc, sizeof(int32_t) * in_ints) != hipSuccess ||
         hipHostMalloc((void**)&m->h_next, sizeof(int32_t) * S) != hipSuccess ||
         hipHostMalloc((void**)&m->h_status, sizeof(int32_t) * 4) != hipSuccess ||
         hipHostMalloc((void**)&m->h_logits, sizeof(float) * (size_t)S * c.vocab) != hipSuccess) {
         set_error(-2, "engine: pinned host allocation failed");
         return -2;
     }
+    m->h_tok = m->h_desc + 3 * S;
     // KV pools start zeroed, like calloc in llama_infer.c:225-226
     if (hipMemset(m->Kpool, 0, kv * sizeof(float)) != hipSuccess ||
         hipMemset(m->Vpool, 0, kv * sizeof(float)) != hipSuccess) {
@@ -212,6 +232,33 @@ int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int 
     return upload(m, &l.w, host, l.bytes());
 }
 
+// Profiling: events recorded on the stream around launches of a class
+// (0 = Q4_K matmul, 1 = attention, 2 = whole step) with the launch's
+// algorithmic bytes; folded into the totals after the step's sync.
+size_t prof_mark(slate_hip_llama* m, hipStream_t s) {
+    if (m->prof_used == m->prof_ev.size()) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return (size_t)-1;
+        m->prof_ev.push_back(e);
+    }
+    size_t i = m->prof_used++;
+    if (hipEventRecord(m->prof_ev[i], s) != hipSuccess) return (size_t)-1;
+    return i;
+}
+
+void prof_collect(slate_hip_llama* m) {
+    for (const auto& r : m->prof_recs) {
+        float ms = 0.f;
+        if (r.e0 == (size_t)-1 || r.e1 == (size_t)-1) continue;
+        if (hipEventElapsedTime(&ms, m->prof_ev[r.e0], m->prof_ev[r.e1]) != hipSuccess) continue;
+        m->prof_ms[r.cls] += ms;
+        m->prof_bytes[r.cls] += r.bytes;
+        m->prof_n[r.cls] += 1;
+    }
+    m->prof_recs.clear();
+    m->prof_used = 0;
+}
+
 // One matmul group: the linears in `lins` read the same input X [T, K] and
 // write column ranges of one partial buffer [S][T_pad][ldo].  Returns S.
 int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const* lins, const int64_t* col,
@@ -223,7 +270,7 @@ int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const*
         anyf |= lins[i]->dtype == DT_F32;
         Mtot += lins[i]->M;
     }
-    const int tpad = (T + 15) / 16 * 16;
+    const int tpad = row_pad(T);
     int S = 1;
     Act16 a = m->act;
     a.rows = T;
@@ -240,9 +287,12 @@ int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const*
     const int64_t ss = (int64_t)tpad * ldo;
     for (int i = 0; i < nl; ++i) {
         const Lin& l = *lins[i];
+        size_t e0 = m->prof_on && l.dtype == DT_Q4K ? prof_mark(m, s) : 0;
         int rc = l.dtype == DT_Q4K ? launch_q4k_mm(l.w, a, m->part + col[i], ldo, ss, l.M, S, s)
                                    : launch_mm_f32(m->part + col[i], X, (const float*)l.w, T, l.M, K, (int)ldo, s);
         if (rc) return rc;
+        if (m->prof_on && l.dtype == DT_Q4K)
+            m->prof_recs.push_back({0, (double)l.bytes() + 4.0 * T * (K + l.M), e0, prof_mark(m, s)});
     }
     *S_out = S;
     return 0;
@@ -255,11 +305,14 @@ int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
     if (l.dtype == DT_Q4K) {
         Act16 a = m->act;
         a.rows = n;
-        a.rows_pad = (n + 15) / 16 * 16;
+        a.rows_pad = row_pad(n);
         a.K = c.d_model;
         int rc = launch_act16_from_f32(a, m->xlast, s);
         if (rc) return rc;
-        return launch_q4k_mm(l.w, a, m->logits, c.vocab, 0, c.vocab, 1, s);
+        size_t e0 = m->prof_on ? prof_mark(m, s) : 0;
+        rc = launch_q4k_mm(l.w, a, m->logits, c.vocab, 0, c.vocab, 1, s);
+        if (m->prof_on) m->prof_recs.push_back({0, (double)l.bytes() + 4.0 * n * (c.d_model + c.vocab), e0, prof_mark(m, s)});
+        return rc;
     }
     return launch_mm_f32(m->logits, m->xlast, (const float*)l.w, n, c.vocab, c.d_model, c.vocab, s);
 }
@@ -268,14 +321,16 @@ int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
 int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t s) {
     const auto& c = m->cfg;
     const int D = c.d_model, H = c.ffn_hidden, hd = c.head_dim, kvd = c.n_kv_heads * hd;
-    SH_CHECK_HIP(hipMemcpyAsync(m->d_desc, m->h_desc, 3 * sizeof(int32_t) * m->max_slots, hipMemcpyHostToDevice, s));
-    SH_CHECK_HIP(hipMemcpyAsync(m->d_tok, m->h_tok, sizeof(int32_t) * T, hipMemcpyHostToDevice, s));
+    size_t estep = m->prof_on ? prof_mark(m, s) : 0;
+    const size_t in_ints = 3 * (size_t)m->max_slots + T + m->n_dec + 2 * (size_t)m->n_pre;
+    SH_CHECK_HIP(hipMemcpyAsync(m->d_desc, m->h_desc, sizeof(int32_t) * in_ints, hipMemcpyHostToDevice, s));
+    const int32_t* d_blk = m->d_tok + T;
     int rc = launch_pack_batch(m->d_desc, m->d_desc + m->max_slots, m->d_desc + 2 * m->max_slots, n, c.max_seq,
                                m->slot_stride, m->max_tokens, m->tok_off, m->tok2seq, m->tok_pos, m->kv_base,
                                m->last_tok, m->status, s);
     if (rc) return rc;
     if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
-    const int tpad = (T + 15) / 16 * 16;
+    const int tpad = row_pad(T);
     int S_prev = 0;
     for (int li = 0; li < c.n_layers; ++li) {
         const LayerDev& Ld = m->L[li];
@@ -295,9 +350,14 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                                         m->tok2seq, m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd,
                                         m->head_stride, m->rope_cs, s)))
             return rc;
-        if ((rc = launch_attention_ragged(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, c.n_heads,
-                                          c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po, m->att_pml, s)))
+        size_t ea = m->prof_on ? prof_mark(m, s) : 0;
+        if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
+                                          m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
+                                          c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
+                                          m->att_pml, s)))
             return rc;
+        if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
+            m->prof_recs.push_back({1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, prof_mark(m, s)});
         {
             const Lin* g[1] = {&Ld.o};
             int64_t col[1] = {0};
@@ -327,6 +387,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, s))) return rc;
     SH_CHECK_HIP(hipMemcpyAsync(m->h_next, m->next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
     SH_CHECK_HIP(hipMemcpyAsync(m->h_status, m->status, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    if (m->prof_on) m->prof_recs.push_back({2, 0.0, estep, prof_mark(m, s)});
     if (want_logits)
         SH_CHECK_HIP(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * (size_t)n * c.vocab,
                                     hipMemcpyDeviceToHost, s));
@@ -466,6 +527,7 @@ slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t*
 void slate_hip_llama_free(slate_hip_llama_t* m) {
     if (!m) return;
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    for (hipEvent_t e : m->prof_ev) (void)hipEventDestroy(e);
     free_model(m);
 }
 
@@ -560,15 +622,48 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
         m->h_desc[2 * m->max_slots + i] = act ? n_new[i] : 0;
     }
     memcpy(m->h_tok, tokens, sizeof(int32_t) * T);
+    // attention work: decode tokens one per block, prompt chunks in blocks of
+    // consecutive tokens of one sequence
+    {
+        const int QB = attn_prefill_block(c.n_heads / c.n_kv_heads);
+        int32_t* blk = m->h_tok + T;
+        int nd = 0, np = 0, t = 0;
+        for (int i = 0; i < n; ++i) {
+            if (n_new[i] == 1) ++nd;
+            else np += (n_new[i] + QB - 1) / QB;
+        }
+        int id = 0, ip = 0;
+        for (int i = 0; i < n; ++i) {
+            if (n_new[i] == 1) {
+                blk[id++] = t;
+            } else {
+                for (int k = 0; k < n_new[i]; k += QB) {
+                    blk[nd + ip] = t + k;
+                    blk[nd + np + ip] = std::min(QB, n_new[i] - k);
+                    ++ip;
+                }
+            }
+            t += n_new[i];
+        }
+        m->n_dec = nd;
+        m->n_pre = np;
+    }
+    m->step_kv_rows = 0;
+    for (int i = 0; i < n; ++i) m->step_kv_rows += (double)sessions[i]->pos + n_new[i];
     hipStream_t s = stream();
     {
         std::lock_guard<std::mutex> lk2(g_enqueue_mu);
         int rc = enqueue_step(m, n, T, out_logits != nullptr, s);
-        if (rc) return rc;
+        if (rc) {
+            m->prof_recs.clear();
+            m->prof_used = 0;
+            return rc;
+        }
         if (hipStreamSynchronize(s) != hipSuccess) {
             set_error(-7, "llama_step: device execution failed");
             return -7;
         }
+        if (m->prof_on) prof_collect(m);
     }
     if (m->h_status[0] != 0) {
         set_error(m->h_status[0], "llama_step: device packing rejected the descriptor (%d)", m->h_status[0]);
@@ -577,6 +672,25 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
     if (out_logits) memcpy(out_logits, m->h_logits, sizeof(float) * (size_t)n * c.vocab);
     if (out_next) memcpy(out_next, m->h_next, sizeof(int32_t) * n);
     for (int i = 0; i < n; ++i) sessions[i]->pos += n_new[i];
+    return 0;
+}
+
+int slate_hip_llama_profile(slate_hip_llama_t* m, int enable) {
+    if (!m) return -1;
+    std::lock_guard<std::mutex> lk(m->mu);
+    m->prof_on = enable != 0;
+    for (int i = 0; i < 3; ++i) m->prof_ms[i] = m->prof_bytes[i] = 0, m->prof_n[i] = 0;
+    m->prof_recs.clear();
+    m->prof_used = 0;
+    return 0;
+}
+
+int slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes, int64_t* launches) {
+    if (!m || cls < 0 || cls > 2) return -1;
+    std::lock_guard<std::mutex> lk(m->mu);
+    if (ms) *ms = m->prof_ms[cls];
+    if (bytes) *bytes = m->prof_bytes[cls];
+    if (launches) *launches = m->prof_n[cls];
     return 0;
 }
 

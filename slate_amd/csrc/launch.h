@@ -30,6 +30,13 @@ int launch_linear_batch(float* C, const float* X, const float* W, int B, int K, 
 
 // k_attn.hip
 int attn_chunk_size();
+int attn_prefill_block(int group);   // query tokens per block for prompt chunks
+// Blocks: dec_t0[n_dec] decode tokens (one each); pre_t0/pre_n[n_pre] runs of
+// consecutive tokens of one sequence.  Every token must be covered once.
+int launch_attention_blocks(float* out, const float* q, const float* Kp, const float* Vp, const int32_t* tok2seq,
+                            const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
+                            int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
+                            int HD, int64_t head_stride, int max_pos, float* po, float* pml, hipStream_t s);
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
 int launch_attention_ragged(float* out, const float* q, const float* Kp, const float* Vp,
                             const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
