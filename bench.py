@@ -141,18 +141,29 @@ def main():
     lib.slate_hip_sync()
     arrivals0 = wl.arrivals
     mixed_steps = 0
+    step_s, step_mixed = [], []
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        mixed_steps += wl.step()[0]
+        ts = time.perf_counter()
+        mixed = wl.step()[0]
+        step_s.append(time.perf_counter() - ts)
+        step_mixed.append(mixed)
+        mixed_steps += mixed
     lib.slate_hip_sync()
     dt = time.perf_counter() - t0
-    prof = m.profile_read()
+    raw = m.profile_read()
     m.profile(False)
     tokens = args.batch * args.steps
     value = tokens / dt
-    log(f"{args.steps} steps in {dt:.3f} s, {mixed_steps} with arrivals ({wl.arrivals - arrivals0} arrivals)")
-    for k, (ms, by, n) in prof.items():
-        log(f"  {k:10s} {ms:9.2f} ms  {n:6d} launches  {by / max(ms, 1e-9) / 1e6:8.1f} GB/s")
+    dec_s = [t for t, mx in zip(step_s, step_mixed) if not mx]
+    mix_s = [t for t, mx in zip(step_s, step_mixed) if mx]
+    log(f"{args.steps} steps in {dt:.3f} s, {mixed_steps} with arrivals ({wl.arrivals - arrivals0} arrivals); "
+        f"decode-only step median {1e3 * np.median(dec_s) if dec_s else 0:.2f} ms, "
+        f"mixed steps {[round(1e3 * t, 1) for t in mix_s]} ms")
+    for k, (ms, by, n) in raw.items():
+        log(f"  {k:13s} {ms:9.2f} ms  {n:6d} launches  {by / max(ms, 1e-9) / 1e6:8.1f} GB/s")
+    # kernel classes over the whole timed region (decode-shaped + prompt-chunk launches)
+    prof = {k: tuple(a + b for a, b in zip(raw[k], raw[k + "_pf"])) for k in ("q4k_mm", "attention", "step")}
 
     # dominant kernel class by device time
     dom = max(("q4k_mm", "attention"), key=lambda k: prof[k][0])

@@ -103,6 +103,15 @@ void  slate_hip_sync(void);                                                     
 /* ---- extensions (device pointers, enqueued on the backend stream) -------- */
 int   slate_hip_matmul_q4k(float* Y, const void* A_q4k, const float* X, int B, int M, int K);
 int   slate_hip_dequant_q4k(float* dst, const void* A_q4k, int64_t n);
+/* Tiled Q4_K: the same blocks regrouped into 16-row tiles so that each
+ * tile's block kb is 2304 contiguous bytes (16 headers, then the nibbles in
+ * the order the matmul lanes read them); rows past M are zero.  It replaces
+ * the row layout of quant.c:135-166 only in device memory owned by the
+ * caller; the values and results are identical.  q4k_tile converts M rows
+ * of K/256 blocks (device src, row layout) into dst of q4k_tiled_bytes. */
+int64_t slate_hip_q4k_tiled_bytes(int M, int K);
+int   slate_hip_q4k_tile(void* dst_tiled, const void* src_q4k, int M, int K);
+int   slate_hip_matmul_q4k_tiled(float* Y, const void* A_tiled, const float* X, int B, int M, int K);
 int   slate_hip_rmsnorm_rows(float* y, const float* x, const float* w, int B, int D, float eps);
 /* RoPE with the angles of llama_infer.c:83-86 (host powf/cosf/sinf table,
  * so identical inputs rotate bit-identically); rows with |pos| >= max_pos
@@ -209,7 +218,10 @@ int   slate_hip_llama_batch_step(slate_hip_llama_t* m, slate_hip_llama_session_t
 int   slate_hip_llama_session_kv(const slate_hip_llama_session_t* s, float* K, float* V);
 
 /* Kernel-class timing with HIP events recorded on the backend stream around
- * each launch: class 0 = Q4_K matmuls, 1 = attention, 2 = whole steps.
+ * each launch: class 0 = Q4_K matmuls of decode shape (<= 16 rows),
+ * 1 = attention in decode-only steps, 2 = decode-only steps, 3 = Q4_K
+ * matmuls over more rows, 4 = attention in steps carrying prompt chunks,
+ * 5 = steps carrying prompt chunks.
  * profile(m, 1) resets the totals and starts recording, profile(m, 0) stops.
  * profile_read returns the summed device milliseconds, the summed
  * algorithmic bytes (weights once, K/V once per kv head and sequence,

@@ -75,6 +75,9 @@ SIGNATURES = {
     "slate_hip_sync": (None, []),
     "slate_hip_matmul_q4k": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int]),
     "slate_hip_dequant_q4k": (C.c_int, [vp, vp, C.c_int64]),
+    "slate_hip_q4k_tiled_bytes": (C.c_int64, [C.c_int, C.c_int]),
+    "slate_hip_q4k_tile": (C.c_int, [vp, vp, C.c_int, C.c_int]),
+    "slate_hip_matmul_q4k_tiled": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int]),
     "slate_hip_rmsnorm_rows": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_float]),
     "slate_hip_rope_rows": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int]),
     "slate_hip_rope_table": (None, [vp, C.c_int, C.c_int, C.c_float]),
@@ -321,9 +324,10 @@ class Llama:
         check(self.lib.slate_hip_llama_profile(self.h, 1 if enable else 0), "profile")
 
     def profile_read(self):
-        """{class: (device ms, algorithmic bytes, launches)} for q4k, attention, step."""
+        """{class: (device ms, algorithmic bytes, launches)}; *_pf classes are
+        launches in steps that carry prompt chunks (or matmuls over > 16 rows)."""
         out = {}
-        for cls, name in enumerate(("q4k_mm", "attention", "step")):
+        for cls, name in enumerate(("q4k_mm", "attention", "step", "q4k_mm_pf", "attention_pf", "step_pf")):
             ms, by, n = C.c_double(), C.c_double(), C.c_int64()
             self.lib.slate_hip_llama_profile_read(self.h, cls, C.byref(ms), C.byref(by), C.byref(n))
             out[name] = (ms.value, by.value, n.value)

@@ -122,14 +122,23 @@ void build_rope_table(float* cs, int max_pos, int hd, float theta) {
     }
 }
 
-// Activation buffers for one Q4_K matmul input of B rows x K.
+// Activation buffers for one Q4_K matmul input of B rows x K (the layout the
+// row count selects).
 int make_act16(Act16& a, int B, int K, int slot) {
     a.rows = B;
     a.rows_pad = row_pad(B);
     a.K = K;
+    a.xh = a.xl = a.ys = nullptr;
+    a.rinv = nullptr;
+    a.frag = nullptr;
+    if (act_is_frag(a)) {
+        a.frag = scratch(slot, act_frag_bytes(K));
+        return a.frag ? 0 : -2;
+    }
     size_t nx = (size_t)a.rows_pad * K;
     size_t ny = (size_t)a.rows_pad * (K / 32) * 2;
-    size_t bytes = nx * 2 * sizeof(_Float16) + ny * sizeof(_Float16) + a.rows_pad * sizeof(float) + 1024;
+    size_t nr = (size_t)(K / QK) * a.rows_pad;
+    size_t bytes = nx * 2 * sizeof(_Float16) + ny * sizeof(_Float16) + nr * sizeof(float) + 1024;
     char* p = (char*)scratch(slot, bytes);
     if (!p) return -2;
     a.xh = (_Float16*)p;
@@ -213,21 +222,43 @@ void slate_hip_linear_batch(float* C, const float* X, const float* W, int B, int
     launch_linear_batch(C, X, W, B, K, N, g_stream);
 }
 
-int slate_hip_matmul_q4k(float* Y, const void* A, const float* X, int B, int M, int K) {
+static int matmul_q4k_common(float* Y, const void* A, const float* X, int B, int M, int K, bool tiled) {
     if (!ensure()) return -7;
     SH_REQUIRE(Y && A && X && B > 0 && M > 0 && K > 0, "matmul_q4k: bad arguments");
     SH_REQUIRE(K % QK == 0, "matmul_q4k: K=%d is not a multiple of 256", K);
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
     Act16 a;
     if (make_act16(a, B, K, 0)) return -2;
-    int rc = launch_act16_from_f32(a, X, g_stream);
+    int rc = launch_act16_from_f32(a, X, K, g_stream);
     if (rc) return rc;
-    int S = q4k_pick_splits(M, K, a.rows_pad);
-    float* part = (float*)scratch(1, (size_t)S * a.rows_pad * M * sizeof(float));
+    const int max_splits = 32;
+    float* part = (float*)scratch(1, (size_t)max_splits * a.rows_pad * M * sizeof(float));
     if (!part) return -2;
-    rc = launch_q4k_mm(A, a, part, (int64_t)M, (int64_t)a.rows_pad * M, M, S, g_stream);
+    Q4kTarget t{A, M, 0};
+    int S = 1;
+    rc = launch_q4k(&t, 1, tiled, a, part, (int64_t)M, (int64_t)a.rows_pad * M, max_splits, &S, g_stream);
     if (rc) return rc;
     return launch_sum_splits(Y, part, S, B, a.rows_pad, M, g_stream);
+}
+
+int slate_hip_matmul_q4k(float* Y, const void* A, const float* X, int B, int M, int K) {
+    return matmul_q4k_common(Y, A, X, B, M, K, false);
+}
+
+int slate_hip_matmul_q4k_tiled(float* Y, const void* A, const float* X, int B, int M, int K) {
+    return matmul_q4k_common(Y, A, X, B, M, K, true);
+}
+
+int64_t slate_hip_q4k_tiled_bytes(int M, int K) {
+    if (M <= 0 || K <= 0 || K % QK) return -1;
+    return (int64_t)q4k_tiled_bytes(M, K);
+}
+
+int slate_hip_q4k_tile(void* dst, const void* src, int M, int K) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(dst && src && M > 0 && K > 0 && K % QK == 0, "q4k_tile: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_q4k_tile(dst, src, M, K, g_stream);
 }
 
 void slate_hip_matvec_q4k(float* y, const void* A, const float* x, int M, int K) {

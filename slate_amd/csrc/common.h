@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
+#include <stdlib.h>
 
 #include "../../include/slate_hip.h"
 
@@ -44,31 +45,52 @@ constexpr int QK = 256;
 constexpr int QBLOCK = 144;
 
 // Activation operand for the Q4_K MFMA kernels: X split into f16 hi + lo with
-// a per-row power-of-two scale, plus per-32-element sums for the min term.
-//   xh, xl : [rows_pad][K]      f16     (x * rscale = hi + lo)
-//   ys     : [rows_pad][K/32][2] f16    (hi, lo) of sum over each sub-block
-//   rinv   : [rows_pad]          f32    1 / rscale
+// a power-of-two scale per 256-element block, plus per-32-element sums for
+// the min term.  Two layouts (k_q4k.hip documents both):
+//   FRAG (rows_pad == 16): frag [K/256][ACT_FRAG_UNITS] 16-byte units in the
+//        order the decode kernel's lanes read them (scales included);
+//   ROW  (rows_pad > 16) : xh, xl [rows_pad][K] f16, ys [rows_pad][K/32][2]
+//        f16, rinv [K/256][rows_pad] f32.
+constexpr int ACT_FRAG_UNITS = 1092;
 struct Act16 {
     _Float16* xh;
     _Float16* xl;
     _Float16* ys;
     float* rinv;
+    void* frag;
     int rows;       // valid rows
     int rows_pad;   // multiple of 16
     int K;
 };
+inline bool act_is_frag(const Act16& a) { return a.rows_pad == 16; }
+inline size_t act_frag_bytes(int K) { return (size_t)(K / QK) * ACT_FRAG_UNITS * 16; }
 
 // Launchers (all enqueue on the given stream; return 0 or negative code).
 int launch_dequant_q4k(float* dst, const void* src, int64_t n_blocks, hipStream_t s);
-int launch_act16_from_f32(const Act16& a, const float* X, hipStream_t s);
-// Split-K partial outputs: element (split, row b, col m) is written to
-// out[split * split_stride + b * ldo + m] for b < rows_pad; with nsplit == 1
-// the single partial is the result.
-int launch_q4k_mm(const void* W, const Act16& a, float* out, int64_t ldo, int64_t split_stride, int M,
-                  int nsplit, hipStream_t s);
+// Rows of X are ldx floats apart.
+int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream_t s);
 int launch_sum_splits(float* Y, const float* part, int nsplit, int rows, int rows_pad, int M,
                       hipStream_t s);
 int q4k_pick_splits(int M, int K, int rows_pad);
+
+// Up to three Q4_K tensors sharing one input, fused into one launch; tensor i
+// writes output columns [col, col + M).  Split-K partials: element (split,
+// row b, col m) goes to out[split * split_stride + b * ldo + m] for
+// b < rows_pad; the split count (<= max_splits) is returned in *S_out.
+struct Q4kTarget { const void* w; int M; int64_t col; };
+struct Q4kTargets {                 // kernel-argument form
+    const uint8_t* w[3];
+    int M[3];
+    int col[3];
+    int grp0[3];                    // first wave group of each tensor
+    int n, grp_end;
+};
+int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo,
+               int64_t split_stride, int max_splits, int* S_out, hipStream_t s);
+// TILED weight layout (16-row tiles, see k_q4k.hip).
+size_t q4k_tiled_bytes(int M, int K);
+int launch_q4k_tile(void* dst, const void* src, int M, int K, hipStream_t s);
+void q4k_untile_host(uint8_t* dst, const uint8_t* src, int M, int K);
 // Activation rows are padded to whole 16-row MFMA tiles, and to whole groups
 // of four tiles beyond 64 rows, so every launch uses a single tile count.
 inline int row_pad(int rows) { return rows <= 64 ? (rows + 15) / 16 * 16 : (rows + 63) / 64 * 64; }

@@ -5,7 +5,9 @@
 // chunks mixed with decode rows).
 //
 // HBM layout:
-//   weights       as given (Q4_K rows of 144-byte blocks, or f32 [out, in])
+//   weights       Q4_K in the TILED layout (16-row tiles, each tile's
+//                 super-block 2304 contiguous bytes; repacked once at load),
+//                 f32 as given [out, in]
 //   K/V pools     [slot][layer][kv_head][max_seq][head_dim] f32
 //   RoPE table    [max_seq][head_dim/2][2] f32 (host-computed angles)
 //   activations   [T][...] f32, packed token-major; split-K partials
@@ -32,12 +34,14 @@ constexpr int DT_F32 = 0;
 constexpr int DT_Q4K = 18;
 
 struct Lin {
-    void* w = nullptr;
+    void* w = nullptr;       // Q4_K: TILED layout
     int dtype = DT_F32;
     int M = 0, K = 0;
+    // bytes of the tensor in slate's own layout (the algorithmic weight bytes)
     size_t bytes() const {
         return dtype == DT_Q4K ? (size_t)M * (K / QK) * QBLOCK : (size_t)M * K * sizeof(float);
     }
+    size_t dev_bytes() const { return dtype == DT_Q4K ? q4k_tiled_bytes(M, K) : bytes(); }
 };
 
 struct LayerDev {
@@ -82,8 +86,9 @@ struct slate_hip_llama {
     std::vector<hipEvent_t> prof_ev;
     size_t prof_used = 0;
     std::vector<ProfRec> prof_recs;
-    double prof_ms[3] = {0, 0, 0}, prof_bytes[3] = {0, 0, 0};
-    int64_t prof_n[3] = {0, 0, 0};
+    static constexpr int NPROF = 6;
+    double prof_ms[NPROF] = {}, prof_bytes[NPROF] = {};
+    int64_t prof_n[NPROF] = {};
     double step_kv_rows = 0;     // sum over sequences of positions attended this step
 };
 
@@ -159,13 +164,16 @@ int alloc_runtime(slate_hip_llama* m) {
     if (dalloc(m, &m->att_po, np)) return -2;
     m->att_pml = m->att_po + (size_t)T * c.n_heads * ((c.max_seq + attn_chunk_size() - 1) / attn_chunk_size()) *
                                  c.head_dim;
-    // Act16 buffers for the widest matmul input (max(D, H)), T_pad rows
+    // Act16 buffers for the widest matmul input (max(D, H)): ROW layout for
+    // T_pad rows, FRAG layout for one 16-row tile
     const int Kmax = std::max(D, H);
     Act16& a = m->act;
     a.K = Kmax;
+    char* fr = nullptr;
     if (dalloc(m, &a.xh, T * Kmax) || dalloc(m, &a.xl, T * Kmax) || dalloc(m, &a.ys, T * (Kmax / 32 + 1) * 2) ||
-        dalloc(m, &a.rinv, T))
+        dalloc(m, &a.rinv, T * (Kmax / QK + 1)) || dalloc(m, &fr, act_frag_bytes(Kmax) + 256))
         return -2;
+    a.frag = fr;
     const int S = m->max_slots;
     const size_t in_ints = 3 * (size_t)S + 4 * T;
     if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
@@ -217,7 +225,40 @@ int upload(slate_hip_llama* m, void** dst, const void* src, size_t bytes) {
     return 0;
 }
 
-int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int K) {
+// Staging buffer for weights in slate's row layout on their way to the
+// TILED layout (grown on demand, released after loading).
+struct RowStage {
+    void* p = nullptr;
+    size_t n = 0;
+    void* get(size_t bytes) {
+        if (bytes <= n) return p;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            set_error(-2, "engine: staging allocation of %zu bytes failed", bytes);
+            return nullptr;
+        }
+        n = bytes;
+        return p;
+    }
+    ~RowStage() {
+        if (p) {
+            (void)hipStreamSynchronize(stream());
+            (void)hipFree(p);
+        }
+    }
+};
+
+// Repack a Q4_K tensor staged in row layout into l.w (TILED).
+int tile_lin(slate_hip_llama* m, Lin& l, const void* row_dev) {
+    char* p;
+    if (dalloc(m, &p, l.dev_bytes())) return -2;
+    l.w = p;
+    return launch_q4k_tile(p, row_dev, l.M, l.K, stream());
+}
+
+int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int K, RowStage& st) {
     l.M = M;
     l.K = K;
     l.dtype = dtype;
@@ -229,7 +270,23 @@ int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int 
         set_error(-1, "engine: Q4_K weight with K=%d (not a multiple of 256)", K);
         return -1;
     }
-    return upload(m, &l.w, host, l.bytes());
+    if (dtype == DT_F32) return upload(m, &l.w, host, l.bytes());
+    if (!host) {
+        set_error(-1, "engine: missing weight pointer");
+        return -1;
+    }
+    // the stream may still be repacking the previous tensor out of the stage
+    if (hipStreamSynchronize(stream()) != hipSuccess) {
+        set_error(-7, "engine: weight repack failed");
+        return -7;
+    }
+    void* row = st.get(l.bytes());
+    if (!row) return -2;
+    if (hipMemcpy(row, host, l.bytes(), hipMemcpyHostToDevice) != hipSuccess) {
+        set_error(-7, "engine: weight upload failed");
+        return -7;
+    }
+    return tile_lin(m, l, row);
 }
 
 // Profiling: events recorded on the stream around launches of a class
@@ -260,39 +317,44 @@ void prof_collect(slate_hip_llama* m) {
 }
 
 // One matmul group: the linears in `lins` read the same input X [T, K] and
-// write column ranges of one partial buffer [S][T_pad][ldo].  Returns S.
+// write column ranges of one partial buffer [S][T_pad][ldo]; *S_out = S.
 int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const* lins, const int64_t* col,
              int nl, int64_t ldo, int* S_out, hipStream_t s) {
     bool anyq = false, anyf = false;
-    int Mtot = 0;
     for (int i = 0; i < nl; ++i) {
         anyq |= lins[i]->dtype == DT_Q4K;
         anyf |= lins[i]->dtype == DT_F32;
-        Mtot += lins[i]->M;
     }
     const int tpad = row_pad(T);
-    int S = 1;
     Act16 a = m->act;
     a.rows = T;
     a.rows_pad = tpad;
     a.K = K;
-    if (anyq) {
-        int rc = launch_act16_from_f32(a, X, s);
-        if (rc) return rc;
-        if (!anyf) {
-            S = q4k_pick_splits(Mtot, K, tpad);
-            while (S > 1 && (size_t)S * tpad * ldo > m->part_floats) --S;
-        }
-    }
     const int64_t ss = (int64_t)tpad * ldo;
+    int max_splits = (int)std::min<size_t>(64, m->part_floats / ((size_t)tpad * ldo));
+    if (anyf) max_splits = 1;
+    int S = 1;
+    if (anyq) {
+        int rc = launch_act16_from_f32(a, X, K, s);
+        if (rc) return rc;
+        Q4kTarget t[3];
+        int nq = 0;
+        double bytes = 4.0 * T * K;
+        for (int i = 0; i < nl; ++i)
+            if (lins[i]->dtype == DT_Q4K) {
+                t[nq++] = Q4kTarget{lins[i]->w, lins[i]->M, col[i]};
+                bytes += (double)lins[i]->bytes() + 4.0 * T * lins[i]->M;
+            }
+        size_t e0 = m->prof_on ? prof_mark(m, s) : 0;
+        rc = launch_q4k(t, nq, true, a, m->part, ldo, ss, max_splits, &S, s);
+        if (rc) return rc;
+        if (m->prof_on) m->prof_recs.push_back({tpad == 16 ? 0 : 3, bytes, e0, prof_mark(m, s)});
+    }
     for (int i = 0; i < nl; ++i) {
         const Lin& l = *lins[i];
-        size_t e0 = m->prof_on && l.dtype == DT_Q4K ? prof_mark(m, s) : 0;
-        int rc = l.dtype == DT_Q4K ? launch_q4k_mm(l.w, a, m->part + col[i], ldo, ss, l.M, S, s)
-                                   : launch_mm_f32(m->part + col[i], X, (const float*)l.w, T, l.M, K, (int)ldo, s);
+        if (l.dtype != DT_F32) continue;
+        int rc = launch_mm_f32(m->part + col[i], X, (const float*)l.w, T, l.M, K, (int)ldo, s);
         if (rc) return rc;
-        if (m->prof_on && l.dtype == DT_Q4K)
-            m->prof_recs.push_back({0, (double)l.bytes() + 4.0 * T * (K + l.M), e0, prof_mark(m, s)});
     }
     *S_out = S;
     return 0;
@@ -307,11 +369,15 @@ int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
         a.rows = n;
         a.rows_pad = row_pad(n);
         a.K = c.d_model;
-        int rc = launch_act16_from_f32(a, m->xlast, s);
+        int rc = launch_act16_from_f32(a, m->xlast, c.d_model, s);
         if (rc) return rc;
         size_t e0 = m->prof_on ? prof_mark(m, s) : 0;
-        rc = launch_q4k_mm(l.w, a, m->logits, c.vocab, 0, c.vocab, 1, s);
-        if (m->prof_on) m->prof_recs.push_back({0, (double)l.bytes() + 4.0 * n * (c.d_model + c.vocab), e0, prof_mark(m, s)});
+        Q4kTarget t{l.w, c.vocab, 0};
+        int S = 1;
+        rc = launch_q4k(&t, 1, true, a, m->logits, c.vocab, 0, 1, &S, s);
+        if (m->prof_on)
+            m->prof_recs.push_back({a.rows_pad == 16 ? 0 : 3, (double)l.bytes() + 4.0 * n * (c.d_model + c.vocab), e0,
+                                    prof_mark(m, s)});
         return rc;
     }
     return launch_mm_f32(m->logits, m->xlast, (const float*)l.w, n, c.vocab, c.d_model, c.vocab, s);
@@ -357,7 +423,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                                           m->att_pml, s)))
             return rc;
         if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
-            m->prof_recs.push_back({1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, prof_mark(m, s)});
+            m->prof_recs.push_back({m->n_pre ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, prof_mark(m, s)});
         {
             const Lin* g[1] = {&Ld.o};
             int64_t col[1] = {0};
@@ -387,7 +453,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, s))) return rc;
     SH_CHECK_HIP(hipMemcpyAsync(m->h_next, m->next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
     SH_CHECK_HIP(hipMemcpyAsync(m->h_status, m->status, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-    if (m->prof_on) m->prof_recs.push_back({2, 0.0, estep, prof_mark(m, s)});
+    if (m->prof_on) m->prof_recs.push_back({m->n_pre ? 5 : 2, 0.0, estep, prof_mark(m, s)});
     if (want_logits)
         SH_CHECK_HIP(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * (size_t)n * c.vocab,
                                     hipMemcpyDeviceToHost, s));
@@ -432,6 +498,7 @@ slate_hip_llama_t* slate_hip_llama_new(const slate_hip_llama_config_t* cfg, cons
     if (new_common(m, cfg, max_slots, max_tokens)) { free_model(m); return nullptr; }
     const auto& c = m->cfg;
     const int D = c.d_model, H = c.ffn_hidden, kvd = c.n_kv_heads * c.head_dim;
+    RowStage st;
     void* p;
     if (upload(m, &p, token_embd, (size_t)c.vocab * D * 4)) { free_model(m); return nullptr; }
     m->tok_embd = (float*)p;
@@ -442,7 +509,7 @@ slate_hip_llama_t* slate_hip_llama_new(const slate_hip_llama_config_t* cfg, cons
         m->out.dtype = DT_F32;
         m->out.M = c.vocab;
         m->out.K = D;
-    } else if (set_lin(m, m->out, output, output_dtype, c.vocab, D)) {
+    } else if (set_lin(m, m->out, output, output_dtype, c.vocab, D, st)) {
         free_model(m);
         return nullptr;
     }
@@ -454,14 +521,21 @@ slate_hip_llama_t* slate_hip_llama_new(const slate_hip_llama_config_t* cfg, cons
         d.attn_norm = (float*)p;
         if (upload(m, &p, s.ffn_norm, (size_t)D * 4)) { free_model(m); return nullptr; }
         d.ffn_norm = (float*)p;
-        if (set_lin(m, d.q, s.attn_q, s.attn_q_dtype, D, D) || set_lin(m, d.k, s.attn_k, s.attn_k_dtype, kvd, D) ||
-            set_lin(m, d.v, s.attn_v, s.attn_v_dtype, kvd, D) ||
-            set_lin(m, d.o, s.attn_output, s.attn_output_dtype, D, D) ||
-            set_lin(m, d.gate, s.ffn_gate, s.ffn_gate_dtype, H, D) || set_lin(m, d.up, s.ffn_up, s.ffn_up_dtype, H, D) ||
-            set_lin(m, d.down, s.ffn_down, s.ffn_down_dtype, D, H)) {
+        if (set_lin(m, d.q, s.attn_q, s.attn_q_dtype, D, D, st) ||
+            set_lin(m, d.k, s.attn_k, s.attn_k_dtype, kvd, D, st) ||
+            set_lin(m, d.v, s.attn_v, s.attn_v_dtype, kvd, D, st) ||
+            set_lin(m, d.o, s.attn_output, s.attn_output_dtype, D, D, st) ||
+            set_lin(m, d.gate, s.ffn_gate, s.ffn_gate_dtype, H, D, st) ||
+            set_lin(m, d.up, s.ffn_up, s.ffn_up_dtype, H, D, st) ||
+            set_lin(m, d.down, s.ffn_down, s.ffn_down_dtype, D, H, st)) {
             free_model(m);
             return nullptr;
         }
+    }
+    if (hipStreamSynchronize(stream()) != hipSuccess) {
+        set_error(-7, "llama_new: weight repack failed");
+        free_model(m);
+        return nullptr;
     }
     return m;
 }
@@ -481,6 +555,7 @@ slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t*
     hipStream_t s = stream();
     uint64_t tid = 0;
     const float std = 0.02f;
+    RowStage st;
     auto gen_lin = [&](Lin& l, int M, int K) -> int {
         l.M = M;
         l.K = K;
@@ -489,12 +564,22 @@ slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t*
             set_error(-1, "llama_new_synthetic: K=%d not a multiple of 256", K);
             return -1;
         }
-        char* p;
-        if (dalloc(m, &p, l.bytes())) return -2;
-        l.w = p;
         uint64_t sd = mix(seed, ++tid);
-        return quant == DT_Q4K ? launch_synth_q4k(p, M, K, sd, std, s)
-                               : launch_synth_f32((float*)p, (int64_t)M * K, sd, std, 0.f, s);
+        if (quant == DT_F32) {
+            char* p;
+            if (dalloc(m, &p, l.bytes())) return -2;
+            l.w = p;
+            return launch_synth_f32((float*)p, (int64_t)M * K, sd, std, 0.f, s);
+        }
+        // generate in row layout (stream-ordered after the previous repack)
+        if (hipStreamSynchronize(s) != hipSuccess) {
+            set_error(-7, "llama_new_synthetic: generation failed");
+            return -7;
+        }
+        void* row = st.get(l.bytes());
+        if (!row) return -2;
+        int rc = launch_synth_q4k(row, M, K, sd, std, s);
+        return rc ? rc : tile_lin(m, l, row);
     };
     auto gen_f32 = [&](float** dst, int64_t n, float sd_std, float fill) -> int {
         if (dalloc(m, dst, (size_t)n)) return -2;
@@ -537,11 +622,17 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
     const void* src = nullptr;
     size_t bytes = 0;
     int dt = DT_F32;
+    const Lin* tiled = nullptr;
     const auto& c = m->cfg;
     std::string n(name);
     if (n == "token_embd") { src = m->tok_embd; bytes = (size_t)c.vocab * c.d_model * 4; }
     else if (n == "output_norm") { src = m->out_norm; bytes = (size_t)c.d_model * 4; }
-    else if (n == "output") { src = m->out.w; bytes = m->out.bytes(); dt = m->out.dtype; }
+    else if (n == "output") {
+        src = m->out.w;
+        bytes = m->out.bytes();
+        dt = m->out.dtype;
+        if (dt == DT_Q4K) tiled = &m->out;
+    }
     else if (n.rfind("blk.", 0) == 0) {
         int li = atoi(n.c_str() + 4);
         size_t dot = n.find('.', 4);
@@ -559,7 +650,12 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
         else if (f == "ffn_up") l = &d.up;
         else if (f == "ffn_down") l = &d.down;
         else return -1;
-        if (l) { src = l->w; bytes = l->bytes(); dt = l->dtype; }
+        if (l) {
+            src = l->w;
+            bytes = l->bytes();
+            dt = l->dtype;
+            if (dt == DT_Q4K) tiled = l;
+        }
     } else {
         return -1;
     }
@@ -567,8 +663,20 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
     if (!host_dst) return (int64_t)bytes;
     if ((int64_t)bytes > cap) return -2;
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
-    if (hipStreamSynchronize(stream()) != hipSuccess ||
-        hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
+    if (hipStreamSynchronize(stream()) != hipSuccess) {
+        set_error(-7, "get_tensor: stream failed");
+        return -7;
+    }
+    if (tiled) {   // back to slate's row layout
+        std::vector<uint8_t> t(tiled->dev_bytes());
+        if (hipMemcpy(t.data(), src, t.size(), hipMemcpyDeviceToHost) != hipSuccess) {
+            set_error(-7, "get_tensor copy failed");
+            return -7;
+        }
+        q4k_untile_host((uint8_t*)host_dst, t.data(), tiled->M, tiled->K);
+        return (int64_t)bytes;
+    }
+    if (hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost) != hipSuccess) {
         set_error(-7, "get_tensor copy failed");
         return -7;
     }
@@ -679,14 +787,14 @@ int slate_hip_llama_profile(slate_hip_llama_t* m, int enable) {
     if (!m) return -1;
     std::lock_guard<std::mutex> lk(m->mu);
     m->prof_on = enable != 0;
-    for (int i = 0; i < 3; ++i) m->prof_ms[i] = m->prof_bytes[i] = 0, m->prof_n[i] = 0;
+    for (int i = 0; i < slate_hip_llama::NPROF; ++i) m->prof_ms[i] = m->prof_bytes[i] = 0, m->prof_n[i] = 0;
     m->prof_recs.clear();
     m->prof_used = 0;
     return 0;
 }
 
 int slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes, int64_t* launches) {
-    if (!m || cls < 0 || cls > 2) return -1;
+    if (!m || cls < 0 || cls >= slate_hip_llama::NPROF) return -1;
     std::lock_guard<std::mutex> lk(m->mu);
     if (ms) *ms = m->prof_ms[cls];
     if (bytes) *bytes = m->prof_bytes[cls];

@@ -5,6 +5,8 @@
 // 12 bytes of packed 6-bit (scale, min) for 8 sub-blocks, 128 bytes of
 // nibbles.  Slate's nibble order: sub-block s owns qs[16s..16s+15]; the low
 // nibble of byte i is element i, the high nibble element i+16.
+#include <string.h>
+
 #include "launch.h"
 
 namespace slate_hip {
@@ -97,64 +99,91 @@ int launch_dequant_q4k(float* dst, const void* src, int64_t n_blocks, hipStream_
 }
 
 // ---------------------------------------------------------------------------
-// Activation split.  Row r of X is scaled by an exact power of two so that
-// max|x| lands in [2^14, 2^15), then split x*s = hi + lo (two f16).  The
-// per-sub-block sums of x*s (<= 2^20) are stored times 2^-6 as hi + lo.
-// Padding rows (r >= rows) are written as zeros.  One workgroup per row.
-__global__ __launch_bounds__(256) void act16_kernel(Act16 a, const float* __restrict__ X) {
-    const int r = blockIdx.x;
-    const int K = a.K;
-    __shared__ float red[256];
-    const float* x = X + (size_t)r * K;
-    bool valid = r < a.rows;
-    float mx = 0.f;
-    if (valid)
-        for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(x[k]));
-    red[threadIdx.x] = mx;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
-        __syncthreads();
-    }
-    mx = red[0];
+// Activation operand.  Each 256-element block of each row is scaled by an
+// exact power of two s so that max|x| over the block lands in [2^14, 2^15),
+// then split x*s = hi + lo (two f16, together exact to ~2^-22 relative).  The
+// per-32-element sums of x*s (<= 2^20) are stored times 2^-6 as hi + lo.
+// Padding rows (r >= rows) are zeros with scale 1.
+//
+// FRAG layout (decode tiles, rows_pad == 16): block kb occupies
+// ACT_FRAG_UNITS 16-byte units ordered exactly as the MFMA lanes read them:
+//   unit (2t + h) * 64 + lane  : x*s hi (h = 0) / lo (h = 1) of row lane&15,
+//                                elements 64*(lane>>4) + 8t .. +7
+//   unit 1024 + lane           : (hi, lo) sums of sub-blocks 4*((lane>>4)&1)
+//                                .. +3 of row lane&15
+//   units 1088 .. 1091         : 1/s of rows 0..15 (f32)
+// ROW layout (prefill, larger batches): xh, xl [rows_pad][K], ys
+// [rows_pad][K/32][2], rinv [K/256][rows_pad].
+typedef _Float16 half4a_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void act16_kernel(Act16 a, const float* __restrict__ X, int64_t ldx, int frag) {
+    const int lane = threadIdx.x & 63;
+    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nblk = a.K / QK;
+    if (kb >= nblk) return;                       // whole wave; no barriers below
+    const int r = blockIdx.y;
+    const bool valid = r < a.rows;
+    float4 v = valid ? *(const float4*)(X + (size_t)r * ldx + (size_t)kb * QK + 4 * lane)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     int ex = 0;
     if (mx > 0.f && isfinite(mx)) {
-        frexpf(mx, &ex);                 // mx = m * 2^ex, m in [0.5, 1)
+        frexpf(mx, &ex);                          // mx = m * 2^ex, m in [0.5, 1)
         ex = 15 - ex;
         ex = ex > 100 ? 100 : (ex < -100 ? -100 : ex);
     }
-    float sc = ldexpf(1.0f, ex);
-    if (threadIdx.x == 0) a.rinv[r] = ldexpf(1.0f, -ex);
-    _Float16* xh = a.xh + (size_t)r * K;
-    _Float16* xl = a.xl + (size_t)r * K;
-    const int nsub = K / 32;
-    // each thread handles whole 32-element sub-blocks
-    for (int sb = threadIdx.x; sb < nsub; sb += 256) {
-        float sum = 0.f;
-#pragma unroll 4
-        for (int e = 0; e < 32; e += 4) {
-            float4 v = valid ? *(const float4*)(x + sb * 32 + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            float vv[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
-            _Float16 h[4], l[4];
+    const float sc = ldexpf(1.0f, ex);
+    const float vv[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+    half4a_t h, l;
+    float sum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                h[i] = (_Float16)vv[i];
-                l[i] = (_Float16)(vv[i] - (float)h[i]);
-                sum += vv[i];
-            }
-            *(half4_t*)(xh + sb * 32 + e) = half4_t{h[0], h[1], h[2], h[3]};
-            *(half4_t*)(xl + sb * 32 + e) = half4_t{l[0], l[1], l[2], l[3]};
+    for (int i = 0; i < 4; ++i) {
+        h[i] = (_Float16)vv[i];
+        l[i] = (_Float16)(vv[i] - (float)h[i]);
+        sum += vv[i];
+    }
+    sum += __shfl_xor(sum, 1, 64);                // 8 lanes = one 32-element sub-block
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    const float ss = sum * (1.0f / 64.0f);
+    const _Float16 sh = (_Float16)ss;
+    const _Float16 sl = (_Float16)(ss - (float)sh);
+    const int sub = lane >> 3;                    // sub-block within the block
+    if (frag) {
+        uint8_t* fb = (uint8_t*)a.frag + (size_t)kb * ACT_FRAG_UNITS * 16;
+        const int g = lane >> 4, t = (lane >> 1) & 7, half_off = 8 * (lane & 1);
+        *(half4a_t*)(fb + ((2 * t) * 64 + 16 * g + r) * 16 + half_off) = h;
+        *(half4a_t*)(fb + ((2 * t + 1) * 64 + 16 * g + r) * 16 + half_off) = l;
+        if ((lane & 7) == 0) {
+            // sub-block s sits in the units of lane groups s>>2 and (s>>2) + 2
+            const int g0 = sub >> 2;
+            const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, sh) |
+                                  ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
+            *(uint32_t*)(fb + (1024 + 16 * g0 + r) * 16 + 4 * (sub & 3)) = pair;
+            *(uint32_t*)(fb + (1024 + 16 * (g0 + 2) + r) * 16 + 4 * (sub & 3)) = pair;
         }
-        float ss = sum * (1.0f / 64.0f);
-        _Float16 sh = (_Float16)ss;
-        _Float16 sl = (_Float16)(ss - (float)sh);
-        a.ys[((size_t)r * nsub + sb) * 2 + 0] = sh;
-        a.ys[((size_t)r * nsub + sb) * 2 + 1] = sl;
+        if (lane == 0) *(float*)(fb + 1088 * 16 + 4 * r) = ldexpf(1.0f, -ex);
+    } else {
+        const size_t off = (size_t)r * a.K + (size_t)kb * QK + 4 * lane;
+        *(half4a_t*)(a.xh + off) = h;
+        *(half4a_t*)(a.xl + off) = l;
+        if ((lane & 7) == 0) {
+            const size_t yo = ((size_t)r * (a.K / 32) + (size_t)kb * 8 + sub) * 2;
+            a.ys[yo] = sh;
+            a.ys[yo + 1] = sl;
+        }
+        if (lane == 0) a.rinv[(size_t)kb * a.rows_pad + r] = ldexpf(1.0f, -ex);
     }
 }
 
-int launch_act16_from_f32(const Act16& a, const float* X, hipStream_t s) {
-    hipLaunchKernelGGL(act16_kernel, dim3(a.rows_pad), dim3(256), 0, s, a, X);
+int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream_t s) {
+    const int nblk = a.K / QK;
+    if (nblk <= 0 || a.rows_pad <= 0) return 0;
+    const bool frag = act_is_frag(a);
+    if (frag && !a.frag) { set_error(-1, "act16: fragment buffer missing"); return -1; }
+    hipLaunchKernelGGL(act16_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, a, X, ldx, frag ? 1 : 0);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -162,21 +191,123 @@ int launch_act16_from_f32(const Act16& a, const float* X, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Dequant-fused Q4_K matmul on MFMA.
 //
-// Y[b, m] = sum_k X[b, k] * W[m, k].  One wave owns a 16-row weight tile and
-// a range of super-blocks; NT tiles of 16 activation rows share each
-// dequantised weight operand.  Per super-block and 32-element K step:
+// Y[b, m] = sum_k X[b, k] * W[m, k].  One wave owns 16-row weight tiles and
+// a range of super-blocks.  Per super-block and 32-element K step:
 //   A (16 act rows x 32 k)   = x*s split into f16 hi and lo (two MFMAs)
 //   B (32 k x 16 weight rows) = q * sc, exact in f16 (q <= 15, sc <= 63)
 // so sum_s sc_s * sum q*x accumulates in f32 inside the MFMA, and is scaled
-// by d once per super-block.  The min term dmin * sum_s mn_s * sum_{i in s} x
-// runs as a 16x16x16 MFMA of the per-sub-block sums against mn (exact).
+// by d (and the block's 1/s) once per super-block.  The min term
+// dmin * sum_s mn_s * sum_{i in s} x runs as a 16x16x16 MFMA of the
+// per-sub-block sums against mn (exact).
 //
 // Lane l: j = l & 15 (weight row of B / activation row of A), g = l >> 4.
 // In step t (0..7) lane group g covers block-local k = 64g + 8t + e, e < 8,
 // i.e. sub-block 2g + t/4, elements 8(t%4)..8(t%4)+7: the low nibbles of
 // bytes 0..7 / 8..15 for t%4 = 0 / 1, the high nibbles for t%4 = 2 / 3.
 // D[i][j] (16x16 f32) sits in lane (j, g) as rows 4g..4g+3.
-template <int NT>
+//
+// Weight layouts:
+//   ROW    slate's own: row m is K/256 consecutive 144-byte blocks.
+//   TILED  16-row tiles (rows past M zero), tile t's block kb is 2304
+//          contiguous bytes at (t * K/256 + kb) * 2304: the 16 rows' 16-byte
+//          headers (d, dmin, scales), then for each lane l the 16 bytes
+//          qs[32g .. 32g+15] of row j, then qs[32g+16 .. 32g+31].  Every load
+//          of a wave is one contiguous 256- or 1024-byte run.
+struct WTile { uint4 hdr, qa, qb; };
+struct ActOp { half8_t h[8], l[8], ys; };
+
+__device__ __forceinline__ void load_wtile(WTile& w, const uint8_t* blk, int g) {
+    w.hdr = *(const uint4*)blk;
+    w.qa = *(const uint4*)(blk + 16 + 32 * g);
+    w.qb = *(const uint4*)(blk + 32 + 32 * g);
+}
+
+__device__ __forceinline__ void load_wtile_tiled(WTile& w, const uint8_t* tb, int lane) {
+    w.hdr = *(const uint4*)(tb + 16 * (lane & 15));
+    w.qa = *(const uint4*)(tb + 256 + 16 * lane);
+    w.qb = *(const uint4*)(tb + 1280 + 16 * lane);
+}
+
+// Row-layout activation operand; branch-free on purpose: a divergent branch
+// around a load makes the compiler wait for every outstanding load (the
+// prefetched block included) at the join.
+__device__ __forceinline__ void load_act(ActOp& A, const Act16& a, int row, int kb, int g) {
+    const size_t off = (size_t)row * a.K + (size_t)kb * QK + 64 * g;
+    const half8_t* xh = (const half8_t*)(a.xh + off);
+    const half8_t* xl = (const half8_t*)(a.xl + off);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) { A.h[t] = xh[t]; A.l[t] = xl[t]; }
+    // lane groups 2, 3 read group (g & 1)'s sums; q4k_block zeroes them (K = 16
+    // padding) where they are used, so no instruction waits on them here
+    A.ys = *(const half8_t*)(a.ys + (((size_t)row * (a.K / 32)) + kb * 8 + 4 * (g & 1)) * 2);
+}
+
+// Hardware half -> float (v_cvt_f32_f16; exact, subnormals included).
+__device__ __forceinline__ float f16_to_f32_hw(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// One super-block of one weight tile against one activation tile.
+__device__ __forceinline__ floatx4 q4k_block(const WTile& w, const ActOp& A, int g) {
+    ScaleBytes sb = unpack_scales(w.hdr.y, w.hdr.z, w.hdr.w);
+    uint32_t scw = g < 2 ? sb.sc_lo : sb.sc_hi;
+    int sh = 16 * (g & 1);
+    _Float16 s0 = (_Float16)(float)((scw >> sh) & 0xffu);
+    _Float16 s1 = (_Float16)(float)((scw >> (sh + 8)) & 0xffu);
+    // q*sc from 1024+q (low nibble) or 1024+16q (high nibble) in one exact fma
+    const half2_t lo_m0 = {s0, s0}, lo_m1 = {s1, s1};
+    const half2_t lo_a0 = lo_m0 * (_Float16)-1024.0f, lo_a1 = lo_m1 * (_Float16)-1024.0f;
+    const half2_t hi_m0 = lo_m0 * (_Float16)0.0625f, hi_m1 = lo_m1 * (_Float16)0.0625f;
+    const half2_t hi_a0 = lo_m0 * (_Float16)-64.0f, hi_a1 = lo_m1 * (_Float16)-64.0f;
+    floatx4 am = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const uint4 Q = t < 4 ? w.qa : w.qb;
+        const int tq = t & 3;
+        const uint32_t mask = (tq & 2) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+        const uint32_t w0 = ((tq & 1) ? Q.z : Q.x) & mask;
+        const uint32_t w1 = ((tq & 1) ? Q.w : Q.y) & mask;
+        const half2_t mul = (tq & 2) ? (t < 4 ? hi_m0 : hi_m1) : (t < 4 ? lo_m0 : lo_m1);
+        const half2_t add = (tq & 2) ? (t < 4 ? hi_a0 : hi_a1) : (t < 4 ? lo_a0 : lo_a1);
+        half2_t p0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u));
+        half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u));
+        half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u));
+        half2_t p3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u));
+        p0 = __builtin_elementwise_fma(p0, mul, add);
+        p1 = __builtin_elementwise_fma(p1, mul, add);
+        p2 = __builtin_elementwise_fma(p2, mul, add);
+        p3 = __builtin_elementwise_fma(p3, mul, add);
+        const half8_t bop = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.h[t], bop, am, 0, 0, 0);
+        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.l[t], bop, am, 0, 0, 0);
+    }
+    // mins of sub-blocks 4g..4g+3 for g < 2 (groups 2, 3 carry the zero padding
+    // on the activation side, so their values do not matter)
+    const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const uint32_t mw = (g & 1) ? sb.mn_hi : sb.mn_lo;
+    const half2_t m01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) + k1024;
+    const half2_t m23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) + k1024;
+    const half4_t bmin = {m01.x, m01.y, m23.x, m23.y};
+    const _Float16 z = (_Float16)0.f;
+    const bool on = g < 2;
+    const half4_t ysh = {on ? A.ys[0] : z, on ? A.ys[2] : z, on ? A.ys[4] : z, on ? A.ys[6] : z};
+    const half4_t ysl = {on ? A.ys[1] : z, on ? A.ys[3] : z, on ? A.ys[5] : z, on ? A.ys[7] : z};
+    floatx4 an = {0.f, 0.f, 0.f, 0.f};
+    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, bmin, an, 0, 0, 0);
+    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, bmin, an, 0, 0, 0);
+    const float d = f16_to_f32_hw(w.hdr.x & 0xffffu);
+    const float dmin64 = f16_to_f32_hw(w.hdr.x >> 16) * 64.0f;
+    floatx4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = d * am[i] - dmin64 * an[i];
+    return r;
+}
+
+// Multi-tile kernel (prefill and batches above 16 rows, ROW activations): a
+// wave owns one 16-row weight tile and NT activation tiles; the weight
+// operand of a block is dequantised once per activation tile, the next
+// block's weights are loaded while the current one is computed.
+template <int NT, bool TILED>
 __global__ __launch_bounds__(256) void q4k_mm_kernel(const uint8_t* __restrict__ W, Act16 a,
                                                      float* __restrict__ out, int64_t ldo,
                                                      int64_t split_stride, int M, int nblk,
@@ -185,103 +316,35 @@ __global__ __launch_bounds__(256) void q4k_mm_kernel(const uint8_t* __restrict__
     const int j = lane & 15;
     const int g = lane >> 4;
     const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int tiles = (M + 15) / 16;
+    if (tile >= tiles) return;
     const int row0 = tile * 16;
-    if (row0 >= M) return;
     const int kb0 = blockIdx.y * blk_per_split;
     const int kb1 = min(kb0 + blk_per_split, nblk);
-    const int wrow = min(row0 + j, M - 1);
-    const int K = a.K;
     const int r0 = rbase + blockIdx.z * NT * 16;      // first activation row of this wave
-    const uint8_t* wbase = W + (size_t)wrow * nblk * QBLOCK;
-
+    const uint8_t* wbase = TILED ? W + (size_t)tile * nblk * (16 * QBLOCK)
+                                 : W + (size_t)min(row0 + j, M - 1) * nblk * QBLOCK;
+    auto ldw = [&](WTile& w, int kb) {
+        if (TILED) load_wtile_tiled(w, wbase + (size_t)kb * (16 * QBLOCK), lane);
+        else load_wtile(w, wbase + (size_t)kb * QBLOCK, g);
+    };
     floatx4 acc[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    WTile wc, wn;
+    if (kb0 < kb1) ldw(wc, kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
-        const uint8_t* blk = wbase + (size_t)kb * QBLOCK;
-        uint4 hdr = *(const uint4*)blk;
-        uint4 qa = *(const uint4*)(blk + 16 + 32 * g);
-        uint4 qb = *(const uint4*)(blk + 32 + 32 * g);
-        ScaleBytes sb = unpack_scales(hdr.y, hdr.z, hdr.w);
-        uint32_t scw = g < 2 ? sb.sc_lo : sb.sc_hi;
-        int sh = 16 * (g & 1);
-        float sc0 = (float)((scw >> sh) & 0xffu);
-        float sc1 = (float)((scw >> (sh + 8)) & 0xffu);
-        // q*sc from 1024+q (low nibble) or 1024+16q (high nibble) in one fma
-        half2_t lo_m0 = {(_Float16)sc0, (_Float16)sc0};
-        half2_t lo_a0 = {(_Float16)(-1024.f * sc0), (_Float16)(-1024.f * sc0)};
-        half2_t hi_m0 = {(_Float16)(sc0 * 0.0625f), (_Float16)(sc0 * 0.0625f)};
-        half2_t hi_a0 = {(_Float16)(-64.f * sc0), (_Float16)(-64.f * sc0)};
-        half2_t lo_m1 = {(_Float16)sc1, (_Float16)sc1};
-        half2_t lo_a1 = {(_Float16)(-1024.f * sc1), (_Float16)(-1024.f * sc1)};
-        half2_t hi_m1 = {(_Float16)(sc1 * 0.0625f), (_Float16)(sc1 * 0.0625f)};
-        half2_t hi_a1 = {(_Float16)(-64.f * sc1), (_Float16)(-64.f * sc1)};
-
-        floatx4 am[NT], an[NT];
-#pragma unroll
-        for (int n = 0; n < NT; ++n) { am[n] = floatx4{0.f, 0.f, 0.f, 0.f}; an[n] = am[n]; }
-
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint4 Q = t < 4 ? qa : qb;
-            const int tq = t & 3;
-            uint32_t w0 = (tq & 1) ? Q.z : Q.x;
-            uint32_t w1 = (tq & 1) ? Q.w : Q.y;
-            uint32_t mask = (tq & 2) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-            w0 &= mask;
-            w1 &= mask;
-            half2_t mul = (tq & 2) ? (t < 4 ? hi_m0 : hi_m1) : (t < 4 ? lo_m0 : lo_m1);
-            half2_t add = (tq & 2) ? (t < 4 ? hi_a0 : hi_a1) : (t < 4 ? lo_a0 : lo_a1);
-            half2_t p0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u));
-            half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u));
-            half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u));
-            half2_t p3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u));
-            p0 = __builtin_elementwise_fma(p0, mul, add);
-            p1 = __builtin_elementwise_fma(p1, mul, add);
-            p2 = __builtin_elementwise_fma(p2, mul, add);
-            p3 = __builtin_elementwise_fma(p3, mul, add);
-            half8_t bop = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                size_t off = (size_t)(r0 + n * 16 + j) * K + (size_t)kb * QK + 64 * g + 8 * t;
-                half8_t ah = *(const half8_t*)(a.xh + off);
-                half8_t al = *(const half8_t*)(a.xl + off);
-                am[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bop, am[n], 0, 0, 0);
-                am[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bop, am[n], 0, 0, 0);
-            }
-        }
-        // min term: K = 16, lane group g holds sub-blocks 4g..4g+3 (g < 2)
-        half4_t bmin = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-        if (g < 2) {
-            uint32_t mw = g == 0 ? sb.mn_lo : sb.mn_hi;
-            half2_t m01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u));
-            half2_t m23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u));
-            m01 = m01 + k1024;
-            m23 = m23 + k1024;
-            bmin = half4_t{m01.x, m01.y, m23.x, m23.y};
-        }
+        ldw(wn, min(kb + 1, kb1 - 1));                  // unconditional prefetch
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
-            half4_t ysh = {(_Float16)0.f, (_Float16)0.f, (_Float16)0.f, (_Float16)0.f};
-            half4_t ysl = ysh;
-            if (g < 2) {
-                const _Float16* yp = a.ys + (((size_t)(r0 + n * 16 + j) * (K / 32)) + kb * 8 + 4 * g) * 2;
-                half8_t v = *(const half8_t*)yp;     // (hi,lo) x 4 sub-blocks
-                ysh = half4_t{v[0], v[2], v[4], v[6]};
-                ysl = half4_t{v[1], v[3], v[5], v[7]};
-            }
-            an[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, bmin, an[n], 0, 0, 0);
-            an[n] = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, bmin, an[n], 0, 0, 0);
+            ActOp A;
+            load_act(A, a, r0 + n * 16 + j, kb, g);
+            const float4 rv = *(const float4*)(a.rinv + (size_t)kb * a.rows_pad + r0 + n * 16 + 4 * g);
+            const floatx4 p = q4k_block(wc, A, g);
+            acc[n] += p * floatx4{rv.x, rv.y, rv.z, rv.w};
         }
-        float d = f16_bits_to_f32(hdr.x & 0xffffu);
-        float dmin64 = f16_bits_to_f32(hdr.x >> 16) * 64.0f;
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[n][r] += d * am[n][r] - dmin64 * an[n][r];
-        }
+        wc = wn;
     }
     if (row0 + j >= M) return;
     float* o = out + (int64_t)blockIdx.y * split_stride;
@@ -290,9 +353,146 @@ __global__ __launch_bounds__(256) void q4k_mm_kernel(const uint8_t* __restrict__
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             int b = r0 + n * 16 + 4 * g + r;
-            o[(int64_t)b * ldo + row0 + j] = acc[n][r] * a.rinv[b];
+            o[(int64_t)b * ldo + row0 + j] = acc[n][r];
         }
     }
+}
+
+// Decode kernel (FRAG activations, one 16-row activation tile).  A workgroup
+// of four waves owns 4R weight tiles (possibly spread over up to three fused
+// tensors) and one split of super-blocks.  The activation units of a block
+// are staged through a double-buffered LDS tile: in each step the workgroup
+// loads the next block's units (issued first, so waiting for them leaves the
+// weight prefetch in flight) and the next block's weights, computes the
+// current block from LDS, then stores the staged units and meets at one
+// barrier.
+template <int R, bool TILED>
+__global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4* __restrict__ frag,
+                                                      float* __restrict__ out, int64_t ldo,
+                                                      int64_t split_stride, int nblk, int bps) {
+    __shared__ uint4 s_act[2][ACT_FRAG_UNITS];
+    constexpr int NF = (ACT_FRAG_UNITS + 255) / 256;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int grp = blockIdx.x * 4 + (tid >> 6);
+    const int ti = (tg.n > 2 && grp >= tg.grp0[2]) ? 2 : ((tg.n > 1 && grp >= tg.grp0[1]) ? 1 : 0);
+    const uint8_t* W = ti == 2 ? tg.w[2] : (ti == 1 ? tg.w[1] : tg.w[0]);
+    const int M = ti == 2 ? tg.M[2] : (ti == 1 ? tg.M[1] : tg.M[0]);
+    const int col = ti == 2 ? tg.col[2] : (ti == 1 ? tg.col[1] : tg.col[0]);
+    const int g0 = ti == 2 ? tg.grp0[2] : (ti == 1 ? tg.grp0[1] : tg.grp0[0]);
+    const int tiles = (M + 15) / 16;
+    const int tile0 = (grp - g0) * R;
+    // waves past the last tile still stage activations and meet the barriers
+    const bool active = grp < tg.grp_end && tile0 < tiles;
+    const int kb0 = blockIdx.y * bps;
+    const int nb = min(kb0 + bps, nblk) - kb0;        // >= 1: the launcher sizes the grid
+    const uint8_t* wp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int t = min(tile0 + r, tiles - 1);
+        wp[r] = TILED ? W + (size_t)t * nblk * (16 * QBLOCK) : W + (size_t)min(t * 16 + j, M - 1) * nblk * QBLOCK;
+    }
+    auto ldw = [&](WTile& w, int r, int kb) {
+        if (TILED) load_wtile_tiled(w, wp[r] + (size_t)kb * (16 * QBLOCK), lane);
+        else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
+    };
+    uint4 fr[NF];
+    WTile wc[R], wn[R];
+    floatx4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    {
+        const uint4* f0 = frag + (size_t)kb0 * ACT_FRAG_UNITS;
+#pragma unroll
+        for (int i = 0; i < NF; ++i) fr[i] = f0[min(tid + 256 * i, ACT_FRAG_UNITS - 1)];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
+#pragma unroll
+    for (int i = 0; i < NF; ++i)
+        if (tid + 256 * i < ACT_FRAG_UNITS) s_act[0][tid + 256 * i] = fr[i];
+    __syncthreads();
+
+    for (int b = 0; b < nb; ++b) {
+        // unconditional (clamped) prefetch: no branch around a load
+        const int kn = kb0 + min(b + 1, nb - 1);
+        const uint4* fn = frag + (size_t)kn * ACT_FRAG_UNITS;
+#pragma unroll
+        for (int i = 0; i < NF; ++i) fr[i] = fn[min(tid + 256 * i, ACT_FRAG_UNITS - 1)];
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint4* sa = s_act[b & 1];
+        if (active) {
+            ActOp A;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                A.h[t] = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
+                A.l[t] = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
+            }
+            A.ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
+            const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
+            const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] += q4k_block(wc[r], A, g) * rs;
+        }
+        if (b + 1 < nb) {
+            uint4* sn = s_act[(b + 1) & 1];
+#pragma unroll
+            for (int i = 0; i < NF; ++i)
+                if (tid + 256 * i < ACT_FRAG_UNITS) sn[tid + 256 * i] = fr[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) wc[r] = wn[r];
+    }
+    if (!active) return;
+    float* o = out + (int64_t)blockIdx.y * split_stride + col;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = (tile0 + r) * 16 + j;
+        if (tile0 + r < tiles && row < M) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[(int64_t)(4 * g + i) * ldo + row] = acc[r][i];
+        }
+    }
+}
+
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
+// Decode plan: the largest R in {4, 2, 1}, then the fewest splits, that give
+// at least `target` workgroups (about two per CU).  Splits keep >= 2 blocks
+// each: a one-block split never overlaps its weight prefetch with compute.
+static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, int* S_out) {
+    static const int R_env = env_int("SLATE_HIP_Q4K_R", 0);
+    static const int S_env = env_int("SLATE_HIP_Q4K_S", 0);
+    static const int target = env_int("SLATE_HIP_Q4K_WGS", 448);
+    if (s_max > nblk / 2) s_max = nblk / 2;
+    if (s_max < 1) s_max = 1;
+    int R_out_v = (R_env == 1 || R_env == 2 || R_env == 4) ? R_env : 1, S_out_v = s_max;
+    bool done = false;
+    for (int R = 4; R >= 1 && !done; R >>= 1) {
+        if ((R_env == 1 || R_env == 2 || R_env == 4) && R != R_env) continue;
+        int groups = 0;
+        for (int i = 0; i < n; ++i) groups += (tiles[i] + R - 1) / R;
+        for (int S = 1; S <= s_max; S *= 2) {
+            if ((groups + 3) / 4 * S >= target) {
+                R_out_v = R;
+                S_out_v = S;
+                done = true;
+                break;
+            }
+        }
+    }
+    if (S_env > 0) S_out_v = S_env < s_max ? S_env : s_max;
+    *R_out = R_out_v;
+    *S_out = S_out_v;
 }
 
 int q4k_pick_splits(int M, int K, int rows_pad) {
@@ -307,27 +507,133 @@ int q4k_pick_splits(int M, int K, int rows_pad) {
     return want;
 }
 
-template <int NT>
+template <int NT, bool TILED>
 static void launch_nt(const uint8_t* w, const Act16& a, float* out, int64_t ldo, int64_t ss, int M, int nblk,
                       int bps, int nsplit, int zgroups, int rbase, hipStream_t s) {
     int tiles = (M + 15) / 16;
     dim3 grid((tiles + 3) / 4, nsplit, zgroups);
-    hipLaunchKernelGGL(q4k_mm_kernel<NT>, grid, dim3(256), 0, s, w, a, out, ldo, ss, M, nblk, bps, rbase);
+    hipLaunchKernelGGL((q4k_mm_kernel<NT, TILED>), grid, dim3(256), 0, s, w, a, out, ldo, ss, M, nblk, bps, rbase);
 }
 
-int launch_q4k_mm(const void* W, const Act16& a, float* out, int64_t ldo, int64_t split_stride, int M,
-                  int nsplit, hipStream_t s) {
-    const int nblk = a.K / QK;
+template <bool TILED>
+static void launch_rows(const uint8_t* w, const Act16& a, float* out, int64_t ldo, int64_t ss, int M, int nblk,
+                        int nsplit, hipStream_t s) {
     const int bps = (nblk + nsplit - 1) / nsplit;
-    const uint8_t* w = (const uint8_t*)W;
     const int ntiles = a.rows_pad / 16;
     const int full = ntiles / 4, rem = ntiles % 4;
-    if (full) launch_nt<4>(w, a, out, ldo, split_stride, M, nblk, bps, nsplit, full, 0, s);
-    if (rem == 1) launch_nt<1>(w, a, out, ldo, split_stride, M, nblk, bps, nsplit, 1, full * 64, s);
-    if (rem == 2) launch_nt<2>(w, a, out, ldo, split_stride, M, nblk, bps, nsplit, 1, full * 64, s);
-    if (rem == 3) launch_nt<3>(w, a, out, ldo, split_stride, M, nblk, bps, nsplit, 1, full * 64, s);
+    if (full) launch_nt<4, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, full, 0, s);
+    if (rem == 1) launch_nt<1, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, 1, full * 64, s);
+    if (rem == 2) launch_nt<2, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, 1, full * 64, s);
+    if (rem == 3) launch_nt<3, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, 1, full * 64, s);
+}
+
+template <int R, bool TILED>
+static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk,
+                       int bps, int nsplit, hipStream_t s) {
+    dim3 grid((tg.grp_end + 3) / 4, nsplit);
+    hipLaunchKernelGGL((q4k_dec_kernel<R, TILED>), grid, dim3(256), 0, s, tg, (const uint4*)a.frag, out, ldo, ss,
+                       nblk, bps);
+}
+
+int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo, int64_t split_stride,
+               int max_splits, int* S_out, hipStream_t s) {
+    if (n < 1 || n > 3) { set_error(-1, "q4k: 1..3 fused tensors"); return -1; }
+    const int nblk = a.K / QK;
+    if (nblk < 1) { set_error(-1, "q4k: K=%d", a.K); return -1; }
+    if (max_splits < 1) max_splits = 1;
+    if (!act_is_frag(a)) {
+        int Mtot = 0;
+        for (int i = 0; i < n; ++i) Mtot += t[i].M;
+        int S = q4k_pick_splits(Mtot, a.K, a.rows_pad);
+        if (S > max_splits) S = max_splits;
+        const int bps = (nblk + S - 1) / S;
+        S = (nblk + bps - 1) / bps;
+        for (int i = 0; i < n; ++i) {
+            if (tiled)
+                launch_rows<true>((const uint8_t*)t[i].w, a, out + t[i].col, ldo, split_stride, t[i].M, nblk, S, s);
+            else
+                launch_rows<false>((const uint8_t*)t[i].w, a, out + t[i].col, ldo, split_stride, t[i].M, nblk, S, s);
+        }
+        SH_CHECK_LAUNCH();
+        *S_out = S;
+        return 0;
+    }
+    int tiles[3];
+    for (int i = 0; i < n; ++i) tiles[i] = (t[i].M + 15) / 16;
+    int R, S;
+    dec_plan(tiles, n, nblk, max_splits, &R, &S);
+    const int bps = (nblk + S - 1) / S;
+    S = (nblk + bps - 1) / bps;                       // every split gets >= 1 block
+    Q4kTargets tg{};
+    int grp = 0;
+    for (int i = 0; i < n; ++i) {
+        tg.w[i] = (const uint8_t*)t[i].w;
+        tg.M[i] = t[i].M;
+        tg.col[i] = (int)t[i].col;
+        tg.grp0[i] = grp;
+        grp += (tiles[i] + R - 1) / R;
+    }
+    tg.n = n;
+    tg.grp_end = grp;
+    if (tiled) {
+        if (R == 4) launch_dec<4, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+        else if (R == 2) launch_dec<2, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+        else launch_dec<1, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+    } else {
+        if (R == 4) launch_dec<4, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+        else if (R == 2) launch_dec<2, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+        else launch_dec<1, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+    }
+    SH_CHECK_LAUNCH();
+    *S_out = S;
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// ROW -> TILED repack: one thread per 16-byte unit of the tiled tensor.
+__global__ __launch_bounds__(256) void q4k_tile_kernel(uint4* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                       int M, int nblk, int64_t units) {
+    const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (u >= units) return;
+    const int64_t tb = u / 144;
+    const int w = (int)(u - tb * 144);
+    const int64_t tile = tb / nblk;
+    const int kb = (int)(tb - tile * nblk);
+    int j, off;
+    if (w < 16) { j = w; off = 0; }
+    else if (w < 80) { const int l = w - 16; j = l & 15; off = 16 + 32 * (l >> 4); }
+    else { const int l = w - 80; j = l & 15; off = 32 + 32 * (l >> 4); }
+    const int64_t row = tile * 16 + j;
+    dst[u] = row < M ? *(const uint4*)(src + (row * nblk + kb) * QBLOCK + off) : make_uint4(0u, 0u, 0u, 0u);
+}
+
+size_t q4k_tiled_bytes(int M, int K) { return (size_t)((M + 15) / 16) * 16 * (size_t)(K / QK) * QBLOCK; }
+
+int launch_q4k_tile(void* dst, const void* src, int M, int K, hipStream_t s) {
+    const int nblk = K / QK;
+    const int64_t units = (int64_t)((M + 15) / 16) * nblk * 144;
+    if (units == 0) return 0;
+    hipLaunchKernelGGL(q4k_tile_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s, (uint4*)dst,
+                       (const uint8_t*)src, M, nblk, units);
     SH_CHECK_LAUNCH();
     return 0;
+}
+
+void q4k_untile_host(uint8_t* dst, const uint8_t* src, int M, int K) {
+    const int nblk = K / QK;
+    for (int64_t row = 0; row < M; ++row) {
+        const int64_t tile = row / 16;
+        const int j = (int)(row % 16);
+        for (int kb = 0; kb < nblk; ++kb) {
+            const uint8_t* tb = src + (tile * nblk + kb) * (16 * QBLOCK);
+            uint8_t* b = dst + (row * nblk + kb) * QBLOCK;
+            memcpy(b, tb + 16 * j, 16);
+            for (int g = 0; g < 4; ++g) {
+                memcpy(b + 16 + 32 * g, tb + 256 + 16 * (16 * g + j), 16);
+                memcpy(b + 32 + 32 * g, tb + 1280 + 16 * (16 * g + j), 16);
+            }
+        }
+    }
 }
 
 // Y[r, m] = sum over splits of part[split][r][m] (fixed order -> deterministic).

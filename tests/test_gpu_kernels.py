@@ -70,7 +70,7 @@ def test_dequant_bitexact_random(hip, orc):
     assert same_floats(got, orc.dequant_q4k(raw, n))
 
 
-@pytest.mark.parametrize("M,K", [(256, 256), (4096, 4096), (1024, 14336)])
+@pytest.mark.parametrize("M,K", [(256, 256), (200, 512), (4096, 4096), (1024, 14336)])
 @pytest.mark.parametrize("B", [1, 3, 16, 17, 64, 70])
 def test_matmul_q4k(hip, orc, M, K, B):
     if M * K > 4096 * 4096 and B > 17:
@@ -96,18 +96,76 @@ def test_matmul_q4k_activation_scales(hip, orc):
     rng = np.random.default_rng(4)
     M, K = 512, 2048
     raw = np.frombuffer(quantize_q4k(rng.normal(0, 0.02, (M, K)).astype(np.float32)), np.uint8).copy()
-    X = rng.normal(0, 1, (5, K)).astype(np.float32)
+    X = rng.normal(0, 1, (6, K)).astype(np.float32)
     X[0] *= 1e-6
     X[1] *= 3e3
     X[2] = 0
     X[3, ::7] *= 100.0
-    Y = DB(5 * M * 4)
-    check(hip.matmul_q4k(Y.p, dev(raw).p, dev(X).p, 5, M, K), "matmul_q4k")
-    got = host(Y, np.float32, (5, M))
-    want = orc.q4k_matmul(raw, X, M, K)
-    for r in (0, 1, 3, 4):
-        assert relerr(got[r], want[r]) < 1e-5, r
-    assert np.all(got[2] == 0)
+    X[5, :256] *= 1e4        # blocks of one row at very different scales
+    X[5, 256:512] *= 1e-4
+    X[5, 1024:1280] = 0
+    for B in (6, 20):        # FRAG (16-row tile) and ROW activation layouts
+        Xb = np.zeros((B, K), np.float32)
+        Xb[:6] = X
+        Y = DB(B * M * 4)
+        check(hip.matmul_q4k(Y.p, dev(raw).p, dev(Xb).p, B, M, K), "matmul_q4k")
+        got = host(Y, np.float32, (B, M))
+        want = orc.q4k_matmul(raw, Xb[:6], M, K)
+        for r in (0, 1, 3, 4, 5):
+            assert relerr(got[r], want[r]) < 1e-5, (B, r)
+        assert np.all(got[2] == 0)
+
+
+def untile_q4k(t, M, K):
+    """Inverse of the TILED layout, written from its definition: tile ti,
+    block kb is 2304 bytes = 16 headers of 16 bytes, then for lane
+    l = 16g + j the 16 bytes qs[32g:32g+16] of row j, then qs[32g+16:32g+32]."""
+    nblk = K // 256
+    tiles = (M + 15) // 16
+    t = t.reshape(tiles, nblk, 2304)
+    out = np.zeros((tiles * 16, nblk, 144), np.uint8)
+    for j in range(16):
+        out[j::16, :, 0:16] = t[:, :, 16 * j:16 * j + 16]
+        for g in range(4):
+            l = 16 * g + j
+            out[j::16, :, 16 + 32 * g:32 + 32 * g] = t[:, :, 256 + 16 * l:272 + 16 * l]
+            out[j::16, :, 32 + 32 * g:48 + 32 * g] = t[:, :, 1280 + 16 * l:1296 + 16 * l]
+    return out, tiles
+
+
+@pytest.mark.parametrize("M,K", [(16, 256), (37, 512), (4096, 4096)])
+def test_q4k_tile_layout(hip, M, K):
+    rng = np.random.default_rng(M + K)
+    raw = tame_random_blocks(rng, M * K // 256)
+    nbytes = hip.lib.slate_hip_q4k_tiled_bytes(M, K)
+    assert nbytes == ((M + 15) // 16) * 16 * (K // 256) * 144
+    T = DB(nbytes)
+    check(hip.lib.slate_hip_q4k_tile(T.p, dev(raw).p, M, K), "q4k_tile")
+    t = host(T, np.uint8, nbytes)
+    rows, tiles = untile_q4k(t, M, K)
+    assert np.array_equal(rows[:M].reshape(-1), raw)
+    assert not rows[M:].any()          # padding rows are zero blocks
+
+
+@pytest.mark.parametrize("M,K,B", [(256, 256, 1), (200, 512, 16), (4096, 4096, 16), (1024, 14336, 7),
+                                   (6144, 4096, 16), (300, 1024, 40), (4096, 4096, 64)])
+def test_matmul_q4k_tiled(hip, orc, M, K, B):
+    """The tiled layout gives the same results as the row layout, bit for
+    bit (same kernels and plan, only the weight addressing differs)."""
+    rng = np.random.default_rng(M * 5 + K + B)
+    W = rng.normal(0, 0.02, (M, K)).astype(np.float32)
+    raw = np.frombuffer(quantize_q4k(W), np.uint8).copy()
+    X = rng.normal(0, 1, (B, K)).astype(np.float32)
+    T = DB(hip.lib.slate_hip_q4k_tiled_bytes(M, K))
+    check(hip.lib.slate_hip_q4k_tile(T.p, dev(raw).p, M, K), "q4k_tile")
+    Yt, Yr = DB(B * M * 4), DB(B * M * 4)
+    Xd = dev(X)
+    check(hip.lib.slate_hip_matmul_q4k_tiled(Yt.p, T.p, Xd.p, B, M, K), "matmul_q4k_tiled")
+    check(hip.matmul_q4k(Yr.p, dev(raw).p, Xd.p, B, M, K), "matmul_q4k")
+    got, row = host(Yt, np.float32, (B, M)), host(Yr, np.float32, (B, M))
+    assert np.array_equal(bits(got), bits(row))
+    if M * K <= 4096 * 4096 and B <= 16:
+        assert relerr(got, orc.q4k_matmul(raw, X, M, K)) < 1e-5
 
 
 def test_matvec_q4k_vtable_golden(hip, golden):
