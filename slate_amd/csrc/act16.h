@@ -1,0 +1,67 @@
+// act16.h -- device-side writer of the Q4_K activation operand, shared by the
+// producers that emit it directly (activation split, fused RMSNorm, SwiGLU and
+// attention merge).
+//
+// Layout: 16-row tiles; tile rt's block kb occupies ACT_FRAG_UNITS 16-byte
+// units at frag + (rt * K/256 + kb) * ACT_FRAG_UNITS, ordered exactly as the
+// MFMA lanes read them (lane = 16 * g + j: row j of the tile, lane group g):
+//   unit (2t + h) * 64 + lane : x*s hi (h = 0) / lo (h = 1), elements
+//                               64g + 8t .. +7 of the block
+//   unit 1024 + lane          : (hi, lo) sums of sub-blocks 4*(g&1) .. +3
+//   units 1088 .. 1091        : 1/s of rows 0..15 (f32); 1092.. padding
+// Each 256-element block of a row has its own exact power-of-two scale s with
+// max|x| * s in [2^14, 2^15); x*s = hi + lo; sub-block sums of x*s are stored
+// times 2^-6 as hi + lo.
+#pragma once
+#include "common.h"
+
+namespace slate_hip {
+
+typedef _Float16 act_half4_t __attribute__((ext_vector_type(4)));
+
+// One wave writes block kb of row r; lane holds elements 4*lane .. 4*lane+3
+// (zeros for padding rows).  Every lane of the wave must call it.
+__device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb, int lane, float4 v) {
+    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    int ex = 0;
+    if (mx > 0.f && isfinite(mx)) {
+        frexpf(mx, &ex);                          // mx = m * 2^ex, m in [0.5, 1)
+        ex = 15 - ex;
+        ex = ex > 100 ? 100 : (ex < -100 ? -100 : ex);
+    }
+    const float sc = ldexpf(1.0f, ex);
+    const float vv[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+    act_half4_t h, l;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[i] = (_Float16)vv[i];
+        l[i] = (_Float16)(vv[i] - (float)h[i]);
+        sum += vv[i];
+    }
+    sum += __shfl_xor(sum, 1, 64);                // 8 lanes = one 32-element sub-block
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    const float ss = sum * (1.0f / 64.0f);
+    const _Float16 sh = (_Float16)ss;
+    const _Float16 sl = (_Float16)(ss - (float)sh);
+    const int sub = lane >> 3;
+    const int rr = r & 15;
+    uint8_t* fb = (uint8_t*)a.frag + ((size_t)(r >> 4) * (a.K / QK) + kb) * ACT_FRAG_UNITS * 16;
+    const int g = lane >> 4, t = (lane >> 1) & 7, half_off = 8 * (lane & 1);
+    *(act_half4_t*)(fb + ((2 * t) * 64 + 16 * g + rr) * 16 + half_off) = h;
+    *(act_half4_t*)(fb + ((2 * t + 1) * 64 + 16 * g + rr) * 16 + half_off) = l;
+    if ((lane & 7) == 0) {
+        // sub-block s sits in the units of lane groups s>>2 and (s>>2) + 2
+        const int g0 = sub >> 2;
+        const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, sh) |
+                              ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
+        *(uint32_t*)(fb + (1024 + 16 * g0 + rr) * 16 + 4 * (sub & 3)) = pair;
+        *(uint32_t*)(fb + (1024 + 16 * (g0 + 2) + rr) * 16 + 4 * (sub & 3)) = pair;
+    }
+    if (lane == 0) *(float*)(fb + 1088 * 16 + 4 * rr) = ldexpf(1.0f, -ex);
+}
+
+}  // namespace slate_hip

@@ -122,31 +122,13 @@ void build_rope_table(float* cs, int max_pos, int hd, float theta) {
     }
 }
 
-// Activation buffers for one Q4_K matmul input of B rows x K (the layout the
-// row count selects).
+// Activation operand buffer for one Q4_K matmul input of B rows x K.
 int make_act16(Act16& a, int B, int K, int slot) {
     a.rows = B;
     a.rows_pad = row_pad(B);
     a.K = K;
-    a.xh = a.xl = a.ys = nullptr;
-    a.rinv = nullptr;
-    a.frag = nullptr;
-    if (act_is_frag(a)) {
-        a.frag = scratch(slot, act_frag_bytes(K));
-        return a.frag ? 0 : -2;
-    }
-    size_t nx = (size_t)a.rows_pad * K;
-    size_t ny = (size_t)a.rows_pad * (K / 32) * 2;
-    size_t nr = (size_t)(K / QK) * a.rows_pad;
-    size_t bytes = nx * 2 * sizeof(_Float16) + ny * sizeof(_Float16) + nr * sizeof(float) + 1024;
-    char* p = (char*)scratch(slot, bytes);
-    if (!p) return -2;
-    a.xh = (_Float16*)p;
-    a.xl = a.xh + nx;
-    a.ys = a.xl + nx;
-    size_t off = ((size_t)((char*)(a.ys + ny) - p) + 255) / 256 * 256;
-    a.rinv = (float*)(p + off);
-    return 0;
+    a.frag = scratch(slot, act_frag_bytes(a.rows_pad, K));
+    return a.frag ? 0 : -2;
 }
 
 }  // namespace slate_hip

@@ -46,24 +46,18 @@ constexpr int QBLOCK = 144;
 
 // Activation operand for the Q4_K MFMA kernels: X split into f16 hi + lo with
 // a power-of-two scale per 256-element block, plus per-32-element sums for
-// the min term.  Two layouts (k_q4k.hip documents both):
-//   FRAG (rows_pad == 16): frag [K/256][ACT_FRAG_UNITS] 16-byte units in the
-//        order the decode kernel's lanes read them (scales included);
-//   ROW  (rows_pad > 16) : xh, xl [rows_pad][K] f16, ys [rows_pad][K/32][2]
-//        f16, rinv [K/256][rows_pad] f32.
-constexpr int ACT_FRAG_UNITS = 1092;
+// the min term, laid out in the order the matmul lanes read them (act16.h):
+// frag [rows_pad/16][K/256][ACT_FRAG_UNITS] 16-byte units.
+constexpr int ACT_FRAG_UNITS = 1152;       // 1092 used, padded to 18 x 64
 struct Act16 {
-    _Float16* xh;
-    _Float16* xl;
-    _Float16* ys;
-    float* rinv;
     void* frag;
     int rows;       // valid rows
     int rows_pad;   // multiple of 16
     int K;
 };
-inline bool act_is_frag(const Act16& a) { return a.rows_pad == 16; }
-inline size_t act_frag_bytes(int K) { return (size_t)(K / QK) * ACT_FRAG_UNITS * 16; }
+inline size_t act_frag_bytes(int rows_pad, int K) {
+    return (size_t)(rows_pad / 16) * (K / QK) * ACT_FRAG_UNITS * 16;
+}
 
 // Launchers (all enqueue on the given stream; return 0 or negative code).
 int launch_dequant_q4k(float* dst, const void* src, int64_t n_blocks, hipStream_t s);
@@ -71,7 +65,6 @@ int launch_dequant_q4k(float* dst, const void* src, int64_t n_blocks, hipStream_
 int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream_t s);
 int launch_sum_splits(float* Y, const float* part, int nsplit, int rows, int rows_pad, int M,
                       hipStream_t s);
-int q4k_pick_splits(int M, int K, int rows_pad);
 
 // Up to three Q4_K tensors sharing one input, fused into one launch; tensor i
 // writes output columns [col, col + M).  Split-K partials: element (split,

@@ -164,16 +164,11 @@ int alloc_runtime(slate_hip_llama* m) {
     if (dalloc(m, &m->att_po, np)) return -2;
     m->att_pml = m->att_po + (size_t)T * c.n_heads * ((c.max_seq + attn_chunk_size() - 1) / attn_chunk_size()) *
                                  c.head_dim;
-    // Act16 buffers for the widest matmul input (max(D, H)): ROW layout for
-    // T_pad rows, FRAG layout for one 16-row tile
+    // Q4_K activation operand for the widest matmul input (max(D, H)), T_pad rows
     const int Kmax = std::max(D, H);
-    Act16& a = m->act;
-    a.K = Kmax;
     char* fr = nullptr;
-    if (dalloc(m, &a.xh, T * Kmax) || dalloc(m, &a.xl, T * Kmax) || dalloc(m, &a.ys, T * (Kmax / 32 + 1) * 2) ||
-        dalloc(m, &a.rinv, T * (Kmax / QK + 1)) || dalloc(m, &fr, act_frag_bytes(Kmax) + 256))
-        return -2;
-    a.frag = fr;
+    if (dalloc(m, &fr, act_frag_bytes((int)T, Kmax))) return -2;
+    m->act = Act16{fr, 0, (int)T, Kmax};
     const int S = m->max_slots;
     const size_t in_ints = 3 * (size_t)S + 4 * T;
     if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
@@ -316,27 +311,37 @@ void prof_collect(slate_hip_llama* m) {
     m->prof_used = 0;
 }
 
-// One matmul group: the linears in `lins` read the same input X [T, K] and
-// write column ranges of one partial buffer [S][T_pad][ldo]; *S_out = S.
-int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const* lins, const int64_t* col,
-             int nl, int64_t ldo, int* S_out, hipStream_t s) {
-    bool anyq = false, anyf = false;
-    for (int i = 0; i < nl; ++i) {
-        anyq |= lins[i]->dtype == DT_Q4K;
-        anyf |= lins[i]->dtype == DT_F32;
-    }
-    const int tpad = row_pad(T);
+// What a matmul group reads: the Q4_K activation operand and/or f32 rows.
+struct GroupIn {
+    bool q4 = false, f32 = false;
+};
+GroupIn group_in(const Lin* const* lins, int nl) {
+    GroupIn g;
+    for (int i = 0; i < nl; ++i) (lins[i]->dtype == DT_Q4K ? g.q4 : g.f32) = true;
+    return g;
+}
+
+// The engine's operand buffer viewed for T rows of width K.
+Act16 act_for(slate_hip_llama* m, int T, int K) {
     Act16 a = m->act;
     a.rows = T;
-    a.rows_pad = tpad;
+    a.rows_pad = row_pad(T);
     a.K = K;
+    return a;
+}
+
+// One matmul group: the linears in `lins` read the same input (operand `a`
+// for Q4_K, rows X [T, K] for f32) and write column ranges of one partial
+// buffer [S][T_pad][ldo]; *S_out = S.
+int mm_group(slate_hip_llama* m, const Act16* a, const float* X, int T, int K, const Lin* const* lins,
+             const int64_t* col, int nl, int64_t ldo, int* S_out, hipStream_t s) {
+    const GroupIn gi = group_in(lins, nl);
+    const int tpad = row_pad(T);
     const int64_t ss = (int64_t)tpad * ldo;
-    int max_splits = (int)std::min<size_t>(64, m->part_floats / ((size_t)tpad * ldo));
-    if (anyf) max_splits = 1;
+    // an f32 linear writes one partial, so a group with one stays unsplit
+    int max_splits = gi.f32 ? 1 : (int)std::min<size_t>(64, m->part_floats / ((size_t)tpad * ldo));
     int S = 1;
-    if (anyq) {
-        int rc = launch_act16_from_f32(a, X, K, s);
-        if (rc) return rc;
+    if (gi.q4) {
         Q4kTarget t[3];
         int nq = 0;
         double bytes = 4.0 * T * K;
@@ -346,7 +351,7 @@ int mm_group(slate_hip_llama* m, const float* X, int T, int K, const Lin* const*
                 bytes += (double)lins[i]->bytes() + 4.0 * T * lins[i]->M;
             }
         size_t e0 = m->prof_on ? prof_mark(m, s) : 0;
-        rc = launch_q4k(t, nq, true, a, m->part, ldo, ss, max_splits, &S, s);
+        int rc = launch_q4k(t, nq, true, *a, m->part, ldo, ss, max_splits, &S, s);
         if (rc) return rc;
         if (m->prof_on) m->prof_recs.push_back({tpad == 16 ? 0 : 3, bytes, e0, prof_mark(m, s)});
     }
@@ -400,52 +405,67 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     int S_prev = 0;
     for (int li = 0; li < c.n_layers; ++li) {
         const LayerDev& Ld = m->L[li];
-        // x (+= down partials of the previous layer) -> xn
-        if ((rc = launch_rmsnorm_rows(m->xn, m->x, li ? m->part : nullptr, S_prev, (int64_t)tpad * D,
-                                      Ld.attn_norm, T, D, c.rms_eps, s)))
-            return rc;
         int S;
+        // x (+= down partials of the previous layer) -> attention norm -> QKV
         {
             const Lin* g[3] = {&Ld.q, &Ld.k, &Ld.v};
             int64_t col[3] = {0, D, D + kvd};
-            if ((rc = mm_group(m, m->xn, T, D, g, col, 3, D + 2 * kvd, &S, s))) return rc;
+            const GroupIn gi = group_in(g, 3);
+            Act16 a = act_for(m, T, D);
+            if ((rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, li ? m->part : nullptr, S_prev,
+                                         (int64_t)tpad * D, Ld.attn_norm, T, D, c.rms_eps, gi.q4 ? &a : nullptr, s)))
+                return rc;
+            if ((rc = mm_group(m, &a, m->xn, T, D, g, col, 3, D + 2 * kvd, &S, s))) return rc;
         }
         float* Kl = m->Kpool + (int64_t)li * m->layer_stride;
         float* Vl = m->Vpool + (int64_t)li * m->layer_stride;
-        if ((rc = launch_rope_kv_append(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
-                                        m->tok2seq, m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd,
-                                        m->head_stride, m->rope_cs, s)))
+        if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd, m->tok2seq,
+                                 m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd, m->head_stride, m->rope_cs,
+                                 s)))
             return rc;
-        size_t ea = m->prof_on ? prof_mark(m, s) : 0;
-        if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
-                                          m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
-                                          c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
-                                          m->att_pml, s)))
-            return rc;
-        if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
-            m->prof_recs.push_back({m->n_pre ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, prof_mark(m, s)});
         {
             const Lin* g[1] = {&Ld.o};
             int64_t col[1] = {0};
-            if ((rc = mm_group(m, m->att, T, D, g, col, 1, D, &S, s))) return rc;
+            const GroupIn gi = group_in(g, 1);
+            Act16 a = act_for(m, T, D);
+            size_t ea = m->prof_on ? prof_mark(m, s) : 0;
+            if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
+                                              m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
+                                              c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
+                                              m->att_pml, gi.q4 ? &a : nullptr, s)))
+                return rc;
+            if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
+                m->prof_recs.push_back(
+                    {m->n_pre ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, prof_mark(m, s)});
+            if ((rc = mm_group(m, &a, m->att, T, D, g, col, 1, D, &S, s))) return rc;
         }
-        if ((rc = launch_rmsnorm_rows(m->xn, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm, T, D, c.rms_eps, s)))
-            return rc;
         {
             const Lin* g[2] = {&Ld.gate, &Ld.up};
             int64_t col[2] = {0, H};
-            if ((rc = mm_group(m, m->xn, T, D, g, col, 2, 2 * H, &S, s))) return rc;
+            const GroupIn gi = group_in(g, 2);
+            Act16 a = act_for(m, T, D);
+            if ((rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm,
+                                         T, D, c.rms_eps, gi.q4 ? &a : nullptr, s)))
+                return rc;
+            if ((rc = mm_group(m, &a, m->xn, T, D, g, col, 2, 2 * H, &S, s))) return rc;
         }
-        if ((rc = launch_silu_mul(m->h, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H, 2 * H, 2 * H, s)))
-            return rc;
         {
             const Lin* g[1] = {&Ld.down};
             int64_t col[1] = {0};
-            if ((rc = mm_group(m, m->h, T, H, g, col, 1, D, &S, s))) return rc;
+            const GroupIn gi = group_in(g, 1);
+            Act16 a = act_for(m, T, H);
+            if (H % QK == 0)
+                rc = launch_silu_act(gi.f32 ? m->h : nullptr, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H,
+                                     2 * H, gi.q4 ? &a : nullptr, s);
+            else   // no Q4_K operand exists for this width
+                rc = launch_silu_mul(m->h, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H, 2 * H, 2 * H, s);
+            if (rc) return rc;
+            if ((rc = mm_group(m, &a, m->h, T, H, g, col, 1, D, &S, s))) return rc;
         }
         S_prev = S;
     }
-    if ((rc = launch_rmsnorm_rows(m->xn, m->x, m->part, S_prev, (int64_t)tpad * D, m->out_norm, T, D, c.rms_eps, s)))
+    if ((rc = launch_rmsnorm_act(m->xn, m->x, m->part, S_prev, (int64_t)tpad * D, m->out_norm, T, D, c.rms_eps,
+                                 nullptr, s)))
         return rc;
     // rows of each sequence's last token -> xlast (gather by last_tok)
     if ((rc = launch_embed_rows(m->xlast, m->xn, m->last_tok, n, T, D, s))) return rc;

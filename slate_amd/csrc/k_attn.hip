@@ -12,6 +12,7 @@
 // running sum, unnormalised output) per (token, q head, chunk); a merge kernel
 // combines the chunks with log-sum-exp rescaling.
 #include "launch.h"
+#include "act16.h"
 
 namespace slate_hip {
 
@@ -172,24 +173,170 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_block_kernel(
     }
 }
 
-// out[t, hq, :] = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c
-__global__ void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ po,
-                                  const float* __restrict__ pml, const int32_t* __restrict__ tok_pos,
-                                  int Hq, int HD, int nch_max) {
-    const int t = blockIdx.x, hq = blockIdx.y;
-    const int L = tok_pos[t] + 1;
-    const int nch = min((L + ATT_CHUNK - 1) / ATT_CHUNK, nch_max);
-    const size_t p0 = ((size_t)t * Hq + hq) * nch_max;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, pml[(p0 + c) * 2]);
-    float den = 0.f;
-    for (int c = 0; c < nch; ++c) den += expf(pml[(p0 + c) * 2] - M) * pml[(p0 + c) * 2 + 1];
-    float inv = 1.0f / den;
-    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-        float acc = 0.f;
-        for (int c = 0; c < nch; ++c) acc += expf(pml[(p0 + c) * 2] - M) * po[(p0 + c) * HD + d];
-        out[((size_t)t * Hq + hq) * HD + d] = acc * inv;
+// Decode work unit (one query token per sequence): (key chunk, token, kv
+// head), G query heads.  Every K and V row of the chunk is read once, whole
+// and coalesced:
+//   scores  8 lanes per key row, lane ls holds dims 32i + 4ls .. +3 of the
+//           row and of the G query slices (each load instruction of a wave
+//           covers 8 rows x 128 contiguous bytes); dot products reduce over
+//           the 8 lanes;
+//   softmax over the chunk (max, exp, sum) per query head in LDS;
+//   PV      HD/4 lanes per V row (64/(HD/4) rows per wave instruction), the
+//           probabilities broadcast from LDS, reduced over lanes and waves.
+// Partials (chunk max m, sum l, unnormalised output) as attn_block_kernel.
+template <int HD, int G>
+__global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
+    const float* __restrict__ q, const float* __restrict__ Kp, const float* __restrict__ Vp,
+    const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
+    const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
+    float* __restrict__ pml) {
+    constexpr int NV = HD / 32;
+    constexpr int LPR = HD / 4;
+    constexpr int KPI = 64 / LPR;
+    __shared__ float sp[G][ATT_CHUNK];
+    __shared__ float4 sred[4][G][LPR];
+    const int c = blockIdx.x, h = blockIdx.z;
+    const int t = dec_t0 ? dec_t0[blockIdx.y] : blockIdx.y;
+    const int p = tok_pos[t];
+    const int k0 = c * ATT_CHUNK;
+    if (k0 > p) return;                            // merge never reads chunks past a token's end
+    const int nk = min(p + 1 - k0, ATT_CHUNK);
+    const int nkp = (nk + 31) & ~31;               // rounds of 32 keys (multiple of 4 * KPI)
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lg = lane >> 3, ls = lane & 7;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int64_t base = kv_base[tok2seq[t]] + (int64_t)h * head_stride + (int64_t)k0 * HD;
+    const float* Kh = Kp + base;
+    const float* Vh = Vp + base;
+    const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
+    float4 qv[G][NV];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+        for (int i = 0; i < NV; ++i) qv[gi][i] = *(const float4*)(qt + gi * HD + 32 * i + 4 * ls);
+
+    // ---- scores
+#pragma unroll 2
+    for (int j0 = 0; j0 < nkp; j0 += 32) {
+        const int j = j0 + 8 * wv + lg;
+        const float* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
+        float4 kv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) kv[i] = *(const float4*)(kr + 32 * i + 4 * ls);
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            float a = 0.f;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                a = __builtin_fmaf(qv[gi][i].x, kv[i].x, a);
+                a = __builtin_fmaf(qv[gi][i].y, kv[i].y, a);
+                a = __builtin_fmaf(qv[gi][i].z, kv[i].z, a);
+                a = __builtin_fmaf(qv[gi][i].w, kv[i].w, a);
+            }
+            a += __shfl_xor(a, 1, 64);
+            a += __shfl_xor(a, 2, 64);
+            a += __shfl_xor(a, 4, 64);
+            if (ls == 0) sp[gi][j] = j < nk ? a * scale : -INFINITY;
+        }
     }
+    __syncthreads();
+    // ---- softmax over the chunk, one wave per query head
+    for (int gi = wv; gi < G; gi += 4) {
+        float mx = -INFINITY;
+        for (int j = lane; j < nkp; j += 64) mx = fmaxf(mx, sp[gi][j]);
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float sum = 0.f;
+        for (int j = lane; j < nkp; j += 64) {
+            const float sc = sp[gi][j];
+            const float e = sc == -INFINITY ? 0.f : expf(sc - mx);
+            sp[gi][j] = e;
+            sum += e;
+        }
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        if (lane == 0) {
+            const size_t pidx = ((size_t)t * Hq + h * G + gi) * nch_max + c;
+            pml[pidx * 2 + 0] = mx;
+            pml[pidx * 2 + 1] = sum;
+        }
+    }
+    __syncthreads();
+    // ---- PV
+    const int kof = lane / LPR, d4 = lane % LPR;
+    float4 acc[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) acc[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int j = wv * KPI + kof; j < nkp; j += 4 * KPI) {
+        const float4 vv = *(const float4*)(Vh + (int64_t)min(j, nk - 1) * HD + 4 * d4);
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            const float pj = sp[gi][j];
+            acc[gi].x = __builtin_fmaf(pj, vv.x, acc[gi].x);
+            acc[gi].y = __builtin_fmaf(pj, vv.y, acc[gi].y);
+            acc[gi].z = __builtin_fmaf(pj, vv.z, acc[gi].z);
+            acc[gi].w = __builtin_fmaf(pj, vv.w, acc[gi].w);
+        }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi)
+        for (int o = LPR; o < 64; o <<= 1) {
+            acc[gi].x += __shfl_xor(acc[gi].x, o, 64);
+            acc[gi].y += __shfl_xor(acc[gi].y, o, 64);
+            acc[gi].z += __shfl_xor(acc[gi].z, o, 64);
+            acc[gi].w += __shfl_xor(acc[gi].w, o, 64);
+        }
+    if (kof == 0)
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) sred[wv][gi][d4] = acc[gi];
+    __syncthreads();
+    for (int idx = tid; idx < G * LPR; idx += ATT_THREADS) {
+        const int gi = idx / LPR, dd = idx - gi * LPR;
+        float4 o = sred[0][gi][dd];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 o2 = sred[w][gi][dd];
+            o.x += o2.x; o.y += o2.y; o.z += o2.z; o.w += o2.w;
+        }
+        const size_t pidx = ((size_t)t * Hq + h * G + gi) * nch_max + c;
+        *(float4*)(po + pidx * HD + 4 * dd) = o;
+    }
+}
+
+// out[t, hq, :] = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c.  One wave per
+// 256 output elements of a token row (lane: 4 consecutive elements of one
+// head); with `act` the row also goes out as the Q4_K activation operand
+// (padding rows t >= T as zeros).
+__global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ po,
+                                                         const float* __restrict__ pml,
+                                                         const int32_t* __restrict__ tok_pos, int T, int Hq,
+                                                         int HD, int nch_max, Act16 a, int act) {
+    const int lane = threadIdx.x & 63;
+    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int D = Hq * HD;
+    if (kb * 256 >= D) return;                     // whole wave
+    const int t = blockIdx.y;
+    const int e = kb * 256 + 4 * lane;
+    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < T && e < D) {
+        const int hq = e / HD, d = e - hq * HD;
+        const int L = tok_pos[t] + 1;
+        const int nch = min((L + ATT_CHUNK - 1) / ATT_CHUNK, nch_max);
+        const size_t p0 = ((size_t)t * Hq + hq) * nch_max;
+        float M = -INFINITY;
+        for (int c = 0; c < nch; ++c) M = fmaxf(M, pml[(p0 + c) * 2]);
+        float den = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c = 0; c < nch; ++c) {
+            const float f = expf(pml[(p0 + c) * 2] - M);
+            den += f * pml[(p0 + c) * 2 + 1];
+            const float4 o = *(const float4*)(po + (p0 + c) * HD + d);
+            acc.x += f * o.x; acc.y += f * o.y; acc.z += f * o.z; acc.w += f * o.w;
+        }
+        const float inv = 1.0f / den;
+        res = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        *(float4*)(out + (size_t)t * D + e) = res;
+    }
+    if (act) act16_store_block(a, t, kb, lane, res);
 }
 
 struct AttnArgs {
@@ -234,13 +381,32 @@ size_t attention_partial_floats(int T, int Hq, int HD, int max_pos) {
     return (size_t)T * Hq * nch * (HD + 2);
 }
 
+template <int HD>
+static int launch_dec_hd(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
+    switch (G) {
+#define SH_DEC(GG)                                                                                            \
+    case GG:                                                                                                  \
+        hipLaunchKernelGGL((attn_dec_kernel<HD, GG>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,  \
+                           a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);    \
+        return 0;
+        SH_DEC(1) SH_DEC(2) SH_DEC(4) SH_DEC(8)
+#undef SH_DEC
+        default: return -5;
+    }
+}
+
 int launch_attention_blocks(float* out, const float* q, const float* Kp, const float* Vp, const int32_t* tok2seq,
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
-                            int HD, int64_t head_stride, int max_pos, float* po, float* pml, hipStream_t s) {
+                            int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
+                            hipStream_t s) {
     if (T <= 0) return 0;
     if (Hkv <= 0 || Hq % Hkv != 0) {
         set_error(-1, "attention: n_q_heads %d not a multiple of n_kv_heads %d", Hq, Hkv);
+        return -1;
+    }
+    if (act && ((Hq * HD) % 256 || act->K != Hq * HD)) {
+        set_error(-1, "attention: operand output needs a row width that is a multiple of 256");
         return -1;
     }
     const int G = Hq / Hkv;
@@ -254,12 +420,17 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
         a.qn = prefill ? pre_n : nullptr;
         dim3 grid(nch_max, nblk, Hkv);
         int rc;
-        switch (HD) {
-            case 16: rc = launch_hd<16>(G, prefill, grid, s, a); break;
-            case 32: rc = launch_hd<32>(G, prefill, grid, s, a); break;
-            case 64: rc = launch_hd<64>(G, prefill, grid, s, a); break;
-            case 128: rc = launch_hd<128>(G, prefill, grid, s, a); break;
-            default: rc = -5;
+        if (!prefill && (HD == 32 || HD == 64 || HD == 128)) {
+            rc = HD == 128 ? launch_dec_hd<128>(G, grid, s, a)
+                           : (HD == 64 ? launch_dec_hd<64>(G, grid, s, a) : launch_dec_hd<32>(G, grid, s, a));
+        } else {
+            switch (HD) {
+                case 16: rc = launch_hd<16>(G, prefill, grid, s, a); break;
+                case 32: rc = launch_hd<32>(G, prefill, grid, s, a); break;
+                case 64: rc = launch_hd<64>(G, prefill, grid, s, a); break;
+                case 128: rc = launch_hd<128>(G, prefill, grid, s, a); break;
+                default: rc = -5;
+            }
         }
         if (rc) {
             set_error(rc, "attention: unsupported head_dim %d / group %d", HD, G);
@@ -267,8 +438,10 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
         }
         SH_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(T, Hq), dim3(HD < 256 ? HD : 256), 0, s, out, po, pml, tok_pos,
-                       Hq, HD, nch_max);
+    const int nb = (Hq * HD + 255) / 256;
+    dim3 mgrid((nb + 3) / 4, act ? act->rows_pad : T);
+    hipLaunchKernelGGL(attn_merge_kernel, mgrid, dim3(256), 0, s, out, po, pml, tok_pos, T, Hq, HD, nch_max,
+                       act ? *act : Act16{}, act ? 1 : 0);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -279,7 +452,7 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
                             int Hq, int Hkv, int HD, int64_t head_stride, int max_pos, float* po,
                             float* pml, hipStream_t s) {
     return launch_attention_blocks(out, q, Kp, Vp, tok2seq, tok_pos, kv_base, T, nullptr, T, nullptr, nullptr, 0,
-                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, s);
+                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include "launch.h"
+#include "act16.h"
 
 namespace slate_hip {
 
@@ -99,91 +100,24 @@ int launch_dequant_q4k(float* dst, const void* src, int64_t n_blocks, hipStream_
 }
 
 // ---------------------------------------------------------------------------
-// Activation operand.  Each 256-element block of each row is scaled by an
-// exact power of two s so that max|x| over the block lands in [2^14, 2^15),
-// then split x*s = hi + lo (two f16, together exact to ~2^-22 relative).  The
-// per-32-element sums of x*s (<= 2^20) are stored times 2^-6 as hi + lo.
-// Padding rows (r >= rows) are zeros with scale 1.
-//
-// FRAG layout (decode tiles, rows_pad == 16): block kb occupies
-// ACT_FRAG_UNITS 16-byte units ordered exactly as the MFMA lanes read them:
-//   unit (2t + h) * 64 + lane  : x*s hi (h = 0) / lo (h = 1) of row lane&15,
-//                                elements 64*(lane>>4) + 8t .. +7
-//   unit 1024 + lane           : (hi, lo) sums of sub-blocks 4*((lane>>4)&1)
-//                                .. +3 of row lane&15
-//   units 1088 .. 1091         : 1/s of rows 0..15 (f32)
-// ROW layout (prefill, larger batches): xh, xl [rows_pad][K], ys
-// [rows_pad][K/32][2], rinv [K/256][rows_pad].
-typedef _Float16 half4a_t __attribute__((ext_vector_type(4)));
-
-__global__ __launch_bounds__(256) void act16_kernel(Act16 a, const float* __restrict__ X, int64_t ldx, int frag) {
+// Activation operand from f32 rows (layout and scaling in act16.h): one wave
+// per 256-element block of a row.
+__global__ __launch_bounds__(256) void act16_kernel(Act16 a, const float* __restrict__ X, int64_t ldx) {
     const int lane = threadIdx.x & 63;
     const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int nblk = a.K / QK;
     if (kb >= nblk) return;                       // whole wave; no barriers below
     const int r = blockIdx.y;
-    const bool valid = r < a.rows;
-    float4 v = valid ? *(const float4*)(X + (size_t)r * ldx + (size_t)kb * QK + 4 * lane)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    int ex = 0;
-    if (mx > 0.f && isfinite(mx)) {
-        frexpf(mx, &ex);                          // mx = m * 2^ex, m in [0.5, 1)
-        ex = 15 - ex;
-        ex = ex > 100 ? 100 : (ex < -100 ? -100 : ex);
-    }
-    const float sc = ldexpf(1.0f, ex);
-    const float vv[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
-    half4a_t h, l;
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        h[i] = (_Float16)vv[i];
-        l[i] = (_Float16)(vv[i] - (float)h[i]);
-        sum += vv[i];
-    }
-    sum += __shfl_xor(sum, 1, 64);                // 8 lanes = one 32-element sub-block
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
-    const float ss = sum * (1.0f / 64.0f);
-    const _Float16 sh = (_Float16)ss;
-    const _Float16 sl = (_Float16)(ss - (float)sh);
-    const int sub = lane >> 3;                    // sub-block within the block
-    if (frag) {
-        uint8_t* fb = (uint8_t*)a.frag + (size_t)kb * ACT_FRAG_UNITS * 16;
-        const int g = lane >> 4, t = (lane >> 1) & 7, half_off = 8 * (lane & 1);
-        *(half4a_t*)(fb + ((2 * t) * 64 + 16 * g + r) * 16 + half_off) = h;
-        *(half4a_t*)(fb + ((2 * t + 1) * 64 + 16 * g + r) * 16 + half_off) = l;
-        if ((lane & 7) == 0) {
-            // sub-block s sits in the units of lane groups s>>2 and (s>>2) + 2
-            const int g0 = sub >> 2;
-            const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, sh) |
-                                  ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
-            *(uint32_t*)(fb + (1024 + 16 * g0 + r) * 16 + 4 * (sub & 3)) = pair;
-            *(uint32_t*)(fb + (1024 + 16 * (g0 + 2) + r) * 16 + 4 * (sub & 3)) = pair;
-        }
-        if (lane == 0) *(float*)(fb + 1088 * 16 + 4 * r) = ldexpf(1.0f, -ex);
-    } else {
-        const size_t off = (size_t)r * a.K + (size_t)kb * QK + 4 * lane;
-        *(half4a_t*)(a.xh + off) = h;
-        *(half4a_t*)(a.xl + off) = l;
-        if ((lane & 7) == 0) {
-            const size_t yo = ((size_t)r * (a.K / 32) + (size_t)kb * 8 + sub) * 2;
-            a.ys[yo] = sh;
-            a.ys[yo + 1] = sl;
-        }
-        if (lane == 0) a.rinv[(size_t)kb * a.rows_pad + r] = ldexpf(1.0f, -ex);
-    }
+    const float4 v = r < a.rows ? *(const float4*)(X + (size_t)r * ldx + (size_t)kb * QK + 4 * lane)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    act16_store_block(a, r, kb, lane, v);
 }
 
 int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream_t s) {
     const int nblk = a.K / QK;
     if (nblk <= 0 || a.rows_pad <= 0) return 0;
-    const bool frag = act_is_frag(a);
-    if (frag && !a.frag) { set_error(-1, "act16: fragment buffer missing"); return -1; }
-    hipLaunchKernelGGL(act16_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, a, X, ldx, frag ? 1 : 0);
+    if (!a.frag || a.rows_pad % 16) { set_error(-1, "act16: bad operand buffer"); return -1; }
+    hipLaunchKernelGGL(act16_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, a, X, ldx);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -228,27 +162,17 @@ __device__ __forceinline__ void load_wtile_tiled(WTile& w, const uint8_t* tb, in
     w.qb = *(const uint4*)(tb + 1280 + 16 * lane);
 }
 
-// Row-layout activation operand; branch-free on purpose: a divergent branch
-// around a load makes the compiler wait for every outstanding load (the
-// prefetched block included) at the join.
-__device__ __forceinline__ void load_act(ActOp& A, const Act16& a, int row, int kb, int g) {
-    const size_t off = (size_t)row * a.K + (size_t)kb * QK + 64 * g;
-    const half8_t* xh = (const half8_t*)(a.xh + off);
-    const half8_t* xl = (const half8_t*)(a.xl + off);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) { A.h[t] = xh[t]; A.l[t] = xl[t]; }
-    // lane groups 2, 3 read group (g & 1)'s sums; q4k_block zeroes them (K = 16
-    // padding) where they are used, so no instruction waits on them here
-    A.ys = *(const half8_t*)(a.ys + (((size_t)row * (a.K / 32)) + kb * 8 + 4 * (g & 1)) * 2);
-}
-
 // Hardware half -> float (v_cvt_f32_f16; exact, subnormals included).
 __device__ __forceinline__ float f16_to_f32_hw(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// One super-block of one weight tile against one activation tile.
-__device__ __forceinline__ floatx4 q4k_block(const WTile& w, const ActOp& A, int g) {
+// Dequantised B operand of one weight tile and block: q * sc for the 8 K
+// steps, the sub-block mins, d and 64 * dmin.
+struct WOp { half8_t b[8]; half4_t bmin; float d, dmin64; };
+
+__device__ __forceinline__ WOp q4k_wop(const WTile& w, int g) {
+    WOp B;
     ScaleBytes sb = unpack_scales(w.hdr.y, w.hdr.z, w.hdr.w);
     uint32_t scw = g < 2 ? sb.sc_lo : sb.sc_hi;
     int sh = 16 * (g & 1);
@@ -259,7 +183,6 @@ __device__ __forceinline__ floatx4 q4k_block(const WTile& w, const ActOp& A, int
     const half2_t lo_a0 = lo_m0 * (_Float16)-1024.0f, lo_a1 = lo_m1 * (_Float16)-1024.0f;
     const half2_t hi_m0 = lo_m0 * (_Float16)0.0625f, hi_m1 = lo_m1 * (_Float16)0.0625f;
     const half2_t hi_a0 = lo_m0 * (_Float16)-64.0f, hi_a1 = lo_m1 * (_Float16)-64.0f;
-    floatx4 am = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
         const uint4 Q = t < 4 ? w.qa : w.qb;
@@ -277,9 +200,7 @@ __device__ __forceinline__ floatx4 q4k_block(const WTile& w, const ActOp& A, int
         p1 = __builtin_elementwise_fma(p1, mul, add);
         p2 = __builtin_elementwise_fma(p2, mul, add);
         p3 = __builtin_elementwise_fma(p3, mul, add);
-        const half8_t bop = {p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.h[t], bop, am, 0, 0, 0);
-        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.l[t], bop, am, 0, 0, 0);
+        B.b[t] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     }
     // mins of sub-blocks 4g..4g+3 for g < 2 (groups 2, 3 carry the zero padding
     // on the activation side, so their values do not matter)
@@ -287,91 +208,61 @@ __device__ __forceinline__ floatx4 q4k_block(const WTile& w, const ActOp& A, int
     const uint32_t mw = (g & 1) ? sb.mn_hi : sb.mn_lo;
     const half2_t m01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) + k1024;
     const half2_t m23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) + k1024;
-    const half4_t bmin = {m01.x, m01.y, m23.x, m23.y};
+    B.bmin = half4_t{m01.x, m01.y, m23.x, m23.y};
+    B.d = f16_to_f32_hw(w.hdr.x & 0xffffu);
+    B.dmin64 = f16_to_f32_hw(w.hdr.x >> 16) * 64.0f;
+    return B;
+}
+
+// One block of one weight tile against one activation tile (before the
+// block's activation scale): d * sum_s sc_s sum q x - 64 dmin * sum_s mn_s ys_s.
+__device__ __forceinline__ floatx4 q4k_mma(const WOp& B, const ActOp& A, int g) {
+    floatx4 am = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.h[t], B.b[t], am, 0, 0, 0);
+        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.l[t], B.b[t], am, 0, 0, 0);
+    }
     const _Float16 z = (_Float16)0.f;
     const bool on = g < 2;
     const half4_t ysh = {on ? A.ys[0] : z, on ? A.ys[2] : z, on ? A.ys[4] : z, on ? A.ys[6] : z};
     const half4_t ysl = {on ? A.ys[1] : z, on ? A.ys[3] : z, on ? A.ys[5] : z, on ? A.ys[7] : z};
     floatx4 an = {0.f, 0.f, 0.f, 0.f};
-    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, bmin, an, 0, 0, 0);
-    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, bmin, an, 0, 0, 0);
-    const float d = f16_to_f32_hw(w.hdr.x & 0xffffu);
-    const float dmin64 = f16_to_f32_hw(w.hdr.x >> 16) * 64.0f;
+    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, B.bmin, an, 0, 0, 0);
+    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, B.bmin, an, 0, 0, 0);
     floatx4 r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = d * am[i] - dmin64 * an[i];
+    for (int i = 0; i < 4; ++i) r[i] = B.d * am[i] - B.dmin64 * an[i];
     return r;
 }
 
-// Multi-tile kernel (prefill and batches above 16 rows, ROW activations): a
-// wave owns one 16-row weight tile and NT activation tiles; the weight
-// operand of a block is dequantised once per activation tile, the next
-// block's weights are loaded while the current one is computed.
-template <int NT, bool TILED>
-__global__ __launch_bounds__(256) void q4k_mm_kernel(const uint8_t* __restrict__ W, Act16 a,
-                                                     float* __restrict__ out, int64_t ldo,
-                                                     int64_t split_stride, int M, int nblk,
-                                                     int blk_per_split, int rbase) {
-    const int lane = threadIdx.x & 63;
-    const int j = lane & 15;
-    const int g = lane >> 4;
-    const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int tiles = (M + 15) / 16;
-    if (tile >= tiles) return;
-    const int row0 = tile * 16;
-    const int kb0 = blockIdx.y * blk_per_split;
-    const int kb1 = min(kb0 + blk_per_split, nblk);
-    const int r0 = rbase + blockIdx.z * NT * 16;      // first activation row of this wave
-    const uint8_t* wbase = TILED ? W + (size_t)tile * nblk * (16 * QBLOCK)
-                                 : W + (size_t)min(row0 + j, M - 1) * nblk * QBLOCK;
-    auto ldw = [&](WTile& w, int kb) {
-        if (TILED) load_wtile_tiled(w, wbase + (size_t)kb * (16 * QBLOCK), lane);
-        else load_wtile(w, wbase + (size_t)kb * QBLOCK, g);
-    };
-    floatx4 acc[NT];
+// Activation operand of one tile-block from its staged units.
+__device__ __forceinline__ void load_act_units(ActOp& A, floatx4& rs, const uint4* sa, int lane) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-    WTile wc, wn;
-    if (kb0 < kb1) ldw(wc, kb0);
-    for (int kb = kb0; kb < kb1; ++kb) {
-        ldw(wn, min(kb + 1, kb1 - 1));                  // unconditional prefetch
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            ActOp A;
-            load_act(A, a, r0 + n * 16 + j, kb, g);
-            const float4 rv = *(const float4*)(a.rinv + (size_t)kb * a.rows_pad + r0 + n * 16 + 4 * g);
-            const floatx4 p = q4k_block(wc, A, g);
-            acc[n] += p * floatx4{rv.x, rv.y, rv.z, rv.w};
-        }
-        wc = wn;
+    for (int t = 0; t < 8; ++t) {
+        A.h[t] = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
+        A.l[t] = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
     }
-    if (row0 + j >= M) return;
-    float* o = out + (int64_t)blockIdx.y * split_stride;
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            int b = r0 + n * 16 + 4 * g + r;
-            o[(int64_t)b * ldo + row0 + j] = acc[n][r];
-        }
-    }
+    A.ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
+    const float4 rv = __builtin_bit_cast(float4, sa[1088 + (lane >> 4)]);
+    rs = floatx4{rv.x, rv.y, rv.z, rv.w};
 }
 
-// Decode kernel (FRAG activations, one 16-row activation tile).  A workgroup
-// of four waves owns 4R weight tiles (possibly spread over up to three fused
-// tensors) and one split of super-blocks.  The activation units of a block
-// are staged through a double-buffered LDS tile: in each step the workgroup
-// loads the next block's units (issued first, so waiting for them leaves the
-// weight prefetch in flight) and the next block's weights, computes the
-// current block from LDS, then stores the staged units and meets at one
-// barrier.
+constexpr int ACT_USED_UNITS = 1092;   // units of a tile-block the kernels read
+
+// Decode kernel (one 16-row activation tile).  A workgroup of four waves
+// owns 4R weight tiles (possibly spread over up to three fused tensors) and
+// one split of super-blocks.  The activation units of a block are staged
+// through a double-buffered LDS tile: in each step the workgroup loads the
+// next block's units (issued first, so waiting for them leaves the weight
+// prefetch in flight) and the next block's weights, computes the current
+// block from LDS, then stores the staged units and meets at one barrier.
 template <int R, bool TILED>
 __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4* __restrict__ frag,
                                                       float* __restrict__ out, int64_t ldo,
                                                       int64_t split_stride, int nblk, int bps) {
-    __shared__ uint4 s_act[2][ACT_FRAG_UNITS];
-    constexpr int NF = (ACT_FRAG_UNITS + 255) / 256;
+    __shared__ uint4 s_act[2][ACT_USED_UNITS];
+    constexpr int NF = (ACT_USED_UNITS + 255) / 256;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int j = lane & 15;
@@ -407,13 +298,13 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
     {
         const uint4* f0 = frag + (size_t)kb0 * ACT_FRAG_UNITS;
 #pragma unroll
-        for (int i = 0; i < NF; ++i) fr[i] = f0[min(tid + 256 * i, ACT_FRAG_UNITS - 1)];
+        for (int i = 0; i < NF; ++i) fr[i] = f0[min(tid + 256 * i, ACT_USED_UNITS - 1)];
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
 #pragma unroll
     for (int i = 0; i < NF; ++i)
-        if (tid + 256 * i < ACT_FRAG_UNITS) s_act[0][tid + 256 * i] = fr[i];
+        if (tid + 256 * i < ACT_USED_UNITS) s_act[0][tid + 256 * i] = fr[i];
     __syncthreads();
 
     for (int b = 0; b < nb; ++b) {
@@ -421,29 +312,22 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
         const int kn = kb0 + min(b + 1, nb - 1);
         const uint4* fn = frag + (size_t)kn * ACT_FRAG_UNITS;
 #pragma unroll
-        for (int i = 0; i < NF; ++i) fr[i] = fn[min(tid + 256 * i, ACT_FRAG_UNITS - 1)];
+        for (int i = 0; i < NF; ++i) fr[i] = fn[min(tid + 256 * i, ACT_USED_UNITS - 1)];
 #pragma unroll
         for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
         __builtin_amdgcn_sched_barrier(0);
-        const uint4* sa = s_act[b & 1];
         if (active) {
             ActOp A;
+            floatx4 rs;
+            load_act_units(A, rs, s_act[b & 1], lane);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                A.h[t] = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
-                A.l[t] = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
-            }
-            A.ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
-            const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
-            const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] += q4k_block(wc[r], A, g) * rs;
+            for (int r = 0; r < R; ++r) acc[r] += q4k_mma(q4k_wop(wc[r], g), A, g) * rs;
         }
         if (b + 1 < nb) {
             uint4* sn = s_act[(b + 1) & 1];
 #pragma unroll
             for (int i = 0; i < NF; ++i)
-                if (tid + 256 * i < ACT_FRAG_UNITS) sn[tid + 256 * i] = fr[i];
+                if (tid + 256 * i < ACT_USED_UNITS) sn[tid + 256 * i] = fr[i];
         }
         __syncthreads();
 #pragma unroll
@@ -457,6 +341,129 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
         if (tile0 + r < tiles && row < M) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[(int64_t)(4 * g + i) * ldo + row] = acc[r][i];
+        }
+    }
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt
+// 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+#define SH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+
+// Direct global -> LDS copy of 16 bytes per lane: lane i's bytes land at LDS
+// byte address lds + 16 i (lds wave-uniform).  Issued from inline assembly
+// so the compiler does not treat every later LDS read as waiting on it (its
+// LDS-DMA tracking would stall the weight prefetch too); callers wait with
+// SH_WAIT_VMCNT and a barrier before reading the copied units.
+__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// Prefill kernel (several 16-row activation tiles).  A workgroup of four
+// waves owns 4R weight tiles of one tensor, NT activation tiles and one split
+// of super-blocks.  Per block, the NT tiles' activation units are copied into
+// one of two LDS buffers by direct global->LDS loads (issued a block ahead,
+// before the weight prefetch, so waiting for them leaves the weights in
+// flight); each wave dequantises its R weight tiles once and runs them
+// against all NT activation tiles.  W and frag are not __restrict__: loads
+// through restrict pointers count as invariant and may be moved across the
+// barriers that order them here.
+template <int R, int NT, bool TILED>
+__global__ __launch_bounds__(256) void q4k_pf_kernel(const uint8_t* W, int M, const uint4* frag, int act_tiles,
+                                                     float* __restrict__ out, int64_t ldo,
+                                                     int64_t split_stride, int nblk, int bps) {
+    __shared__ uint4 s_act[2 * NT * ACT_FRAG_UNITS];
+    constexpr int CHUNKS = NT * ACT_FRAG_UNITS / 64;  // 1 KiB wave copies per block
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int j = lane & 15;
+    const int g = lane >> 4;
+    const int wv = tid >> 6;
+    const int tiles = (M + 15) / 16;
+    const int tile0 = (blockIdx.x * 4 + wv) * R;
+    const bool active = tile0 < tiles;
+    const int at0 = blockIdx.z * NT;
+    const int kb0 = blockIdx.y * bps;
+    const int nb = min(kb0 + bps, nblk) - kb0;        // >= 1: the launcher sizes the grid
+    const uint8_t* wp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int t = min(tile0 + r, tiles - 1);
+        wp[r] = TILED ? W + (size_t)t * nblk * (16 * QBLOCK) : W + (size_t)min(t * 16 + j, M - 1) * nblk * QBLOCK;
+    }
+    auto ldw = [&](WTile& w, int r, int kb) {
+        if (TILED) load_wtile_tiled(w, wp[r] + (size_t)kb * (16 * QBLOCK), lane);
+        else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
+    };
+    // copy block kb of activation tiles at0 .. at0+NT-1 (clamped) into `dst`
+    // (every address stays inside the operand buffer: at < act_tiles, kb < nblk)
+    auto stage = [&](uint4* dst, int kb) {
+        for (int c = wv; c < CHUNKS; c += 4) {
+            const int n = c / (ACT_FRAG_UNITS / 64);
+            const int u = (c - n * (ACT_FRAG_UNITS / 64)) * 64;
+            const int at = min(at0 + n, act_tiles - 1);
+            const uint4* src = frag + ((size_t)at * nblk + kb) * ACT_FRAG_UNITS + u + lane;
+            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + n * ACT_FRAG_UNITS + u)));
+        }
+    };
+    WTile wc[R], wn[R];
+    floatx4 acc[R][NT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    stage(s_act, kb0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
+    __builtin_amdgcn_sched_barrier(0);
+    SH_WAIT_VMCNT(0);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        // compute block b from one buffer while the other receives block b+1
+        const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
+        const int kn = kb0 + min(b + 1, nb - 1);
+        if (b + 1 < nb) stage(s_act + ((b + 1) & 1) * NT * ACT_FRAG_UNITS, kn);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
+        __builtin_amdgcn_sched_barrier(0);
+        if (active) {
+            WOp B[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) B[r] = q4k_wop(wc[r], g);
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                ActOp A;
+                floatx4 rs;
+                load_act_units(A, rs, cur + n * ACT_FRAG_UNITS, lane);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][n] += q4k_mma(B[r], A, g) * rs;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // the next block's units and weights have landed: waiting for the
+        // weights here (not at their first use) keeps the compiler's in-order
+        // load counting from also waiting on the next step's LDS copies
+        SH_WAIT_VMCNT(0);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) wc[r] = wn[r];
+    }
+    if (!active) return;
+    float* o = out + (int64_t)blockIdx.y * split_stride;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int row = (tile0 + r) * 16 + j;
+        if (tile0 + r >= tiles || row >= M) continue;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            if (at0 + n >= act_tiles) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[(int64_t)((at0 + n) * 16 + 4 * g + i) * ldo + row] = acc[r][n][i];
         }
     }
 }
@@ -495,38 +502,6 @@ static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, i
     *S_out = S_out_v;
 }
 
-int q4k_pick_splits(int M, int K, int rows_pad) {
-    int tiles = (M + 15) / 16;
-    int nblk = K / QK;
-    int groups = (rows_pad + 63) / 64;
-    int waves = tiles * groups;
-    int want = (2048 + waves - 1) / waves;     // aim for >= 2048 waves
-    if (want > 16) want = 16;
-    if (want > nblk) want = nblk;
-    if (want < 1) want = 1;
-    return want;
-}
-
-template <int NT, bool TILED>
-static void launch_nt(const uint8_t* w, const Act16& a, float* out, int64_t ldo, int64_t ss, int M, int nblk,
-                      int bps, int nsplit, int zgroups, int rbase, hipStream_t s) {
-    int tiles = (M + 15) / 16;
-    dim3 grid((tiles + 3) / 4, nsplit, zgroups);
-    hipLaunchKernelGGL((q4k_mm_kernel<NT, TILED>), grid, dim3(256), 0, s, w, a, out, ldo, ss, M, nblk, bps, rbase);
-}
-
-template <bool TILED>
-static void launch_rows(const uint8_t* w, const Act16& a, float* out, int64_t ldo, int64_t ss, int M, int nblk,
-                        int nsplit, hipStream_t s) {
-    const int bps = (nblk + nsplit - 1) / nsplit;
-    const int ntiles = a.rows_pad / 16;
-    const int full = ntiles / 4, rem = ntiles % 4;
-    if (full) launch_nt<4, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, full, 0, s);
-    if (rem == 1) launch_nt<1, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, 1, full * 64, s);
-    if (rem == 2) launch_nt<2, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, 1, full * 64, s);
-    if (rem == 3) launch_nt<3, TILED>(w, a, out, ldo, ss, M, nblk, bps, nsplit, 1, full * 64, s);
-}
-
 template <int R, bool TILED>
 static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk,
                        int bps, int nsplit, hipStream_t s) {
@@ -535,24 +510,45 @@ static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t
                        nblk, bps);
 }
 
+constexpr int PF_R = 2;
+
+template <int NT, bool TILED>
+static void launch_pf(const Q4kTarget& t, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk, int bps,
+                      int nsplit, hipStream_t s) {
+    const int tiles = (t.M + 15) / 16;
+    const int act_tiles = a.rows_pad / 16;
+    dim3 grid((tiles + 4 * PF_R - 1) / (4 * PF_R), nsplit, (act_tiles + NT - 1) / NT);
+    hipLaunchKernelGGL((q4k_pf_kernel<PF_R, NT, TILED>), grid, dim3(256), 0, s, (const uint8_t*)t.w, t.M,
+                       (const uint4*)a.frag, act_tiles, out + t.col, ldo, ss, nblk, bps);
+}
+
 int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo, int64_t split_stride,
                int max_splits, int* S_out, hipStream_t s) {
     if (n < 1 || n > 3) { set_error(-1, "q4k: 1..3 fused tensors"); return -1; }
     const int nblk = a.K / QK;
     if (nblk < 1) { set_error(-1, "q4k: K=%d", a.K); return -1; }
+    if (!a.frag || a.rows_pad < 16 || a.rows_pad % 16) { set_error(-1, "q4k: bad operand buffer"); return -1; }
     if (max_splits < 1) max_splits = 1;
-    if (!act_is_frag(a)) {
-        int Mtot = 0;
-        for (int i = 0; i < n; ++i) Mtot += t[i].M;
-        int S = q4k_pick_splits(Mtot, a.K, a.rows_pad);
-        if (S > max_splits) S = max_splits;
+    const int act_tiles = a.rows_pad / 16;
+    if (act_tiles > 1) {
+        // prefill: NT activation tiles per workgroup, splits only to fill the chip
+        static const int pf_target = env_int("SLATE_HIP_Q4K_PF_WGS", 256);
+        const int NT = act_tiles >= 4 ? 4 : (act_tiles >= 2 ? 2 : 1);
+        int wgs = 0;
+        for (int i = 0; i < n; ++i)
+            wgs += ((t[i].M + 15) / 16 + 4 * PF_R - 1) / (4 * PF_R) * ((act_tiles + NT - 1) / NT);
+        int S = 1;
+        while (S * 2 <= max_splits && S * 2 <= nblk / 2 && wgs * S < pf_target) S *= 2;
         const int bps = (nblk + S - 1) / S;
         S = (nblk + bps - 1) / bps;
         for (int i = 0; i < n; ++i) {
-            if (tiled)
-                launch_rows<true>((const uint8_t*)t[i].w, a, out + t[i].col, ldo, split_stride, t[i].M, nblk, S, s);
-            else
-                launch_rows<false>((const uint8_t*)t[i].w, a, out + t[i].col, ldo, split_stride, t[i].M, nblk, S, s);
+            if (NT == 4) {
+                if (tiled) launch_pf<4, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
+                else launch_pf<4, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
+            } else {
+                if (tiled) launch_pf<2, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
+                else launch_pf<2, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
+            }
         }
         SH_CHECK_LAUNCH();
         *S_out = S;

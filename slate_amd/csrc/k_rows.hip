@@ -2,6 +2,7 @@
 // KV append, embedding gather, greedy argmax, ragged-batch packing and the
 // small f32 matmuls behind the vtable's matvec / linear_batch.
 #include "launch.h"
+#include "act16.h"
 
 namespace slate_hip {
 
@@ -161,47 +162,209 @@ int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int 
     return 0;
 }
 
-// Fused epilogue of the QKV projection for a ragged step: sums split-K
-// partials of [T, D + 2*kv_dim], rotates q and k at each token's position,
-// writes q to qout and appends k, v into the sequence's KV cache
-// (pool layout [slot][layer][kv_head][max_seq][hd]).
-__global__ __launch_bounds__(256) void rope_kv_append_kernel(
-    float* __restrict__ qout, float* __restrict__ Kpool, float* __restrict__ Vpool,
-    const float* __restrict__ part, int nsplit, int64_t split_stride, int qkv_ld,
-    const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
-    const int64_t* __restrict__ kv_base, int n_heads, int n_kv_heads, int hd, int64_t head_stride,
-    const float* __restrict__ cs) {
-    extern __shared__ float row[];      // D + 2*kv_dim floats
-    const int t = blockIdx.x;
-    const int D = n_heads * hd, kvd = n_kv_heads * hd;
-    const float* pr = part + (size_t)t * qkv_ld;
-    for (int c = threadIdx.x; c < D + 2 * kvd; c += blockDim.x) {
-        float v = pr[c];
-        for (int k = 1; k < nsplit; ++k) v += pr[(int64_t)k * split_stride + c];
-        row[c] = v;
+// ---------------------------------------------------------------------------
+// Engine epilogues that also emit the next Q4_K matmul's activation operand
+// (act16.h), so a split-K sum, the row operation and the operand conversion
+// are one pass over the row.
+
+// sum_{k < n} p[k * stride] in split order, loads issued eight at a time so
+// the latency of the partials is paid once per batch, not once per split.
+__device__ __forceinline__ float4 split_sum4(const float* p, int n, int64_t stride) {
+    float4 s = *(const float4*)p;
+    int k = 1;
+    for (; k + 8 <= n; k += 8) {
+        float4 t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = *(const float4*)(p + (int64_t)(k + i) * stride);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { s.x += t[i].x; s.y += t[i].y; s.z += t[i].z; s.w += t[i].w; }
     }
+    for (; k < n; ++k) {
+        const float4 t = *(const float4*)(p + (int64_t)k * stride);
+        s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+    }
+    return s;
+}
+
+__device__ __forceinline__ float split_sum1(const float* p, int n, int64_t stride) {
+    float s = p[0];
+    int k = 1;
+    for (; k + 8 <= n; k += 8) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = p[(int64_t)(k + i) * stride];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += t[i];
+    }
+    for (; k < n; ++k) s += p[(int64_t)k * stride];
+    return s;
+}
+
+// Residual + RMSNorm: x += sum_s delta[s] (fixed split order, written back),
+// y = (x * w) * inv with inv = 1/sqrtf((float)(sum x^2 / D) + eps)
+// (backend_cpu.c:48-76), stored as f32 (y != nullptr) and/or as the operand
+// (act != 0, D % 256 == 0).  One workgroup per row keeps the row in
+// registers: thread i owns elements 4(i + nt*c) .. +3 of chunk c, so each
+// wave owns whole 256-element blocks.  Rows >= rows write zero operand rows.
+constexpr int RMS_MAX_CHUNKS = 4;
+__global__ __launch_bounds__(1024) void rmsnorm_act_kernel(float* __restrict__ y, float* __restrict__ x,
+                                                           const float* __restrict__ delta, int nsplit,
+                                                           int64_t split_stride, const float* __restrict__ w,
+                                                           int rows, int D, float eps, Act16 a, int act) {
+#pragma clang fp contract(off)
+    __shared__ double sh[16];
+    const int r = blockIdx.x;
+    const int nt = blockDim.x, tid = threadIdx.x, lane = tid & 63;
+    const bool valid = r < rows;
+    float4 v[RMS_MAX_CHUNKS];
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < RMS_MAX_CHUNKS; ++c) {
+        v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int e = 4 * (tid + nt * c);
+        if (valid && e < D) {
+            float* xr = x + (size_t)r * D + e;
+            float4 xv = *(const float4*)xr;
+            if (delta) {
+                const float4 sm = split_sum4(delta + (size_t)r * D + e, nsplit, split_stride);
+                xv.x += sm.x; xv.y += sm.y; xv.z += sm.z; xv.w += sm.w;
+                *(float4*)xr = xv;
+            }
+            v[c] = xv;
+            acc = __builtin_fmaf(xv.x, xv.x, acc);
+            acc = __builtin_fmaf(xv.y, xv.y, acc);
+            acc = __builtin_fmaf(xv.z, xv.z, acc);
+            acc = __builtin_fmaf(xv.w, xv.w, acc);
+        }
+    }
+    double sq = (double)acc;
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if (lane == 0) sh[tid >> 6] = sq;
     __syncthreads();
-    const int p = tok_pos[t];
-    rope_apply(row, n_heads, hd, p, cs, threadIdx.x, blockDim.x);
-    rope_apply(row + D, n_kv_heads, hd, p, cs, threadIdx.x, blockDim.x);
-    __syncthreads();
-    for (int c = threadIdx.x; c < D; c += blockDim.x) qout[(size_t)t * D + c] = row[c];
-    const int64_t base = kv_base[tok2seq[t]];
-    for (int c = threadIdx.x; c < kvd; c += blockDim.x) {
-        int h = c / hd, d = c - h * hd;
-        int64_t off = base + (int64_t)h * head_stride + (int64_t)p * hd + d;
-        Kpool[off] = row[D + c];
-        Vpool[off] = row[D + kvd + c];
+    sq = 0.0;
+    for (int i = 0; i < (nt >> 6); ++i) sq += sh[i];
+    const float inv = 1.0f / sqrtf((float)(sq / (double)D) + eps);
+#pragma unroll
+    for (int c = 0; c < RMS_MAX_CHUNKS; ++c) {
+        const int e = 4 * (tid + nt * c);
+        if (e >= D) break;                        // uniform per wave when D % 256 == 0
+        float4 yv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (valid) {
+            const float4 wv = *(const float4*)(w + e);
+            yv = make_float4((v[c].x * wv.x) * inv, (v[c].y * wv.y) * inv, (v[c].z * wv.z) * inv,
+                             (v[c].w * wv.w) * inv);
+            if (y) *(float4*)(y + (size_t)r * D + e) = yv;
+        }
+        if (act) act16_store_block(a, r, e / QK, lane, yv);
     }
 }
 
-int launch_rope_kv_append(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit,
-                          int64_t split_stride, int qkv_ld, const int32_t* tok2seq,
-                          const int32_t* tok_pos, const int64_t* kv_base, int T, int n_heads,
-                          int n_kv_heads, int hd, int64_t head_stride, const float* cs, hipStream_t s) {
+int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64_t split_stride, const float* w,
+                       int rows, int D, float eps, const Act16* a, hipStream_t s) {
+    if (rows <= 0) return 0;
+    if (D % 4 || D > 4 * 1024 * RMS_MAX_CHUNKS || (a && (D % QK || a->K != D))) {
+        set_error(-1, "rmsnorm_act: unsupported width %d", D);
+        return -1;
+    }
+    int nt = (D / 4 + RMS_MAX_CHUNKS - 1) / RMS_MAX_CHUNKS;
+    nt = (nt + 63) / 64 * 64;
+    if (nt > 1024) nt = 1024;
+    if (nt < 64) nt = 64;
+    const int grid = a ? a->rows_pad : rows;
+    hipLaunchKernelGGL(rmsnorm_act_kernel, dim3(grid), dim3(nt), 0, s, y, x, delta, nsplit, split_stride, w, rows,
+                       D, eps, a ? *a : Act16{}, a ? 1 : 0);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// SwiGLU of split-K gate/up partials, h = silu(g) * u with g = sum_s gate[s],
+// u = sum_s up[s] (backend_cpu.c:78-97 semantics, expf form), stored as f32
+// (y != nullptr, [rows][H]) and/or as the operand of the down projection.
+// One wave per 256-element block of a row (H % 256 == 0).
+__global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, const float* __restrict__ gate,
+                                                       const float* __restrict__ up, int rows, int H, int nsplit,
+                                                       int64_t split_stride, int64_t ld, Act16 a, int act) {
+    const int lane = threadIdx.x & 63;
+    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (kb * QK >= H) return;                     // whole wave
+    const int r = blockIdx.y;
+    const int e = kb * QK + 4 * lane;
+    float4 h = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < rows) {
+        const float* gp = gate + (size_t)r * ld + e;
+        const float* upp = up + (size_t)r * ld + e;
+        const float4 g = split_sum4(gp, nsplit, split_stride), u = split_sum4(upp, nsplit, split_stride);
+        h = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
+                        (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
+        if (y) *(float4*)(y + (size_t)r * H + e) = h;
+    }
+    if (act) act16_store_block(a, r, kb, lane, h);
+}
+
+int launch_silu_act(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
+                    int64_t split_stride, int64_t ld, const Act16* a, hipStream_t s) {
+    if (rows <= 0) return 0;
+    if (H % QK || (a && a->K != H)) {
+        set_error(-1, "silu_act: width %d is not a multiple of 256", H);
+        return -1;
+    }
+    const int nblk = H / QK;
+    dim3 grid((nblk + 3) / 4, a ? a->rows_pad : rows);
+    hipLaunchKernelGGL(silu_act_kernel, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride, ld,
+                       a ? *a : Act16{}, a ? 1 : 0);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+// QKV epilogue, one wave per (token, head): sums the split-K partials of the
+// head's columns, rotates q / k at the token's position (same table and
+// expressions as rope_apply) and writes q to qout, k and v into the KV pool.
+__global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, float* __restrict__ Kpool,
+                                                     float* __restrict__ Vpool, const float* __restrict__ part,
+                                                     int nsplit, int64_t split_stride, int qkv_ld,
+                                                     const int32_t* __restrict__ tok2seq,
+                                                     const int32_t* __restrict__ tok_pos,
+                                                     const int64_t* __restrict__ kv_base, int n_heads,
+                                                     int n_kv_heads, int hd, int64_t head_stride,
+                                                     const float* __restrict__ cs) {
+#pragma clang fp contract(off)
+    const int u = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int D = n_heads * hd, kvd = n_kv_heads * hd, half = hd / 2;
+    const int p = tok_pos[t];
+    const int ap = p < 0 ? -p : p;
+    const float sg = p < 0 ? -1.0f : 1.0f;
+    const float* pr = part + (size_t)t * qkv_ld;
+    auto col = [&](int c) { return split_sum1(pr + c, nsplit, split_stride); };
+    if (u < n_heads) {
+        for (int i = lane; i < half; i += 64) {
+            const int c0 = u * hd + i;
+            const float a = col(c0), b = col(c0 + half);
+            const float c = cs[((size_t)ap * half + i) * 2 + 0];
+            const float sn = sg * cs[((size_t)ap * half + i) * 2 + 1];
+            qout[(size_t)t * D + c0] = a * c - b * sn;
+            qout[(size_t)t * D + c0 + half] = a * sn + b * c;
+        }
+    } else {
+        const int kh = u - n_heads;
+        const int64_t base = kv_base[tok2seq[t]] + (int64_t)kh * head_stride + (int64_t)p * hd;
+        for (int i = lane; i < half; i += 64) {
+            const int ck = D + kh * hd + i, cv = D + kvd + kh * hd + i;
+            const float a = col(ck), b = col(ck + half);
+            const float c = cs[((size_t)ap * half + i) * 2 + 0];
+            const float sn = sg * cs[((size_t)ap * half + i) * 2 + 1];
+            Kpool[base + i] = a * c - b * sn;
+            Kpool[base + i + half] = a * sn + b * c;
+            Vpool[base + i] = col(cv);
+            Vpool[base + i + half] = col(cv + half);
+        }
+    }
+}
+
+int launch_rope_kv(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit, int64_t split_stride,
+                   int qkv_ld, const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
+                   int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, hipStream_t s) {
     if (T <= 0) return 0;
-    size_t shm = (size_t)(n_heads + 2 * n_kv_heads) * hd * sizeof(float);
-    hipLaunchKernelGGL(rope_kv_append_kernel, dim3(T), dim3(256), shm, s, qout, Kpool, Vpool, part,
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout, Kpool, Vpool, part,
                        nsplit, split_stride, qkv_ld, tok2seq, tok_pos, kv_base, n_heads, n_kv_heads, hd,
                        head_stride, cs);
     SH_CHECK_LAUNCH();
@@ -211,33 +374,46 @@ int launch_rope_kv_append(float* qout, float* Kpool, float* Vpool, const float* 
 // ---------------------------------------------------------------------------
 // Greedy argmax per row with sampling.c:14-18 semantics: the first maximal
 // element wins (strict '>'), NaN is never selected unless element 0 is NaN,
-// in which case nothing compares greater and index 0 is returned.
-__global__ __launch_bounds__(256) void argmax_rows_kernel(int32_t* __restrict__ out,
-                                                          const float* __restrict__ logits, int V) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
+// in which case nothing compares greater and index 0 is returned.  1024
+// threads per row; thread i scans float4 groups i, i + 1024, ... in order,
+// then a tree keeps the larger value, or the lower index on ties.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(int32_t* __restrict__ out,
+                                                           const float* __restrict__ logits, int V) {
+    __shared__ float sv[1024];
+    __shared__ int si[1024];
     const float* p = logits + (size_t)blockIdx.x * V;
+    const int tid = threadIdx.x;
     float bv = -INFINITY;
     int bi = -1;
-    for (int i = threadIdx.x; i < V; i += 256) {
-        float v = p[i];
+    auto take = [&](float v, int i) {
         if (v > bv || (bi < 0 && !(v != v))) { bv = v; bi = i; }
+    };
+    const bool al = ((uintptr_t)p & 15) == 0;
+    const int nv4 = al ? V / 4 : 0;
+#pragma unroll 4
+    for (int q = tid; q < nv4; q += 1024) {
+        const float4 v = *(const float4*)(p + 4 * q);
+        take(v.x, 4 * q);
+        take(v.y, 4 * q + 1);
+        take(v.z, 4 * q + 2);
+        take(v.w, 4 * q + 3);
     }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
+    for (int i = 4 * nv4 + tid; i < V; i += 1024) take(p[i], i);
+    sv[tid] = bv;
+    si[tid] = bi;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) {
-            float v2 = sv[threadIdx.x + o];
-            int i2 = si[threadIdx.x + o];
-            float v1 = sv[threadIdx.x];
-            int i1 = si[threadIdx.x];
-            bool take = i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1));
-            if (take) { sv[threadIdx.x] = v2; si[threadIdx.x] = i2; }
+    for (int o = 512; o > 0; o >>= 1) {
+        if (tid < o) {
+            float v2 = sv[tid + o];
+            int i2 = si[tid + o];
+            float v1 = sv[tid];
+            int i1 = si[tid];
+            bool tk = i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1));
+            if (tk) { sv[tid] = v2; si[tid] = i2; }
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         float p0 = p[0];
         out[blockIdx.x] = (p0 != p0 || si[0] < 0) ? 0 : si[0];
     }
@@ -245,7 +421,7 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(int32_t* __restrict__ 
 
 int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, hipStream_t s) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(256), 0, s, out, logits, V);
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(1024), 0, s, out, logits, V);
     SH_CHECK_LAUNCH();
     return 0;
 }
