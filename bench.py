@@ -12,11 +12,14 @@ each step produces one token per sequence.
 
 Printed: one JSON line.  value = generated tokens / wall time over K timed
 steps (weights and KV resident in HBM).  roofline = the dominant kernel class
-(Q4_K matmul or attention) by device time, from HIP events recorded on the
-backend stream around every launch in the timed steps: achieved = algorithmic
-bytes / device time.  cpu_baseline = slate's own C decode step
-(slate_llama_decode_step, single thread as wired) on the same weights and KV
-state, for one step of all 16 sequences.
+of the decode steps by device time (decode-shaped Q4_K matmuls or decode
+attention), from HIP events recorded on the backend stream around every
+launch in the timed steps: achieved = algorithmic bytes / device time;
+traffic = HBM bytes per launch from the committed rocprofv3 PMC summary.
+cpu_baseline = slate's own C decode step (slate_llama_decode_step, single
+thread as wired) on the same weights and KV state, for one step of all 16
+sequences.  --copy-calibration instead runs a plain device copy of known
+size (for scaling the PMC byte counters).
 """
 import argparse
 import json
@@ -114,7 +117,19 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 1 GiB device-to-device copy 5 times and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = 1 << 28                                  # 2^28 f32 = 1 GiB each way
+        a = torch.ones(n, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 5}))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU sharding is described "
                                    "in DESIGN.md and not executed", "n_gpus": args.gpus}))
@@ -162,21 +177,21 @@ def main():
         f"mixed steps {[round(1e3 * t, 1) for t in mix_s]} ms")
     for k, (ms, by, n) in raw.items():
         log(f"  {k:13s} {ms:9.2f} ms  {n:6d} launches  {by / max(ms, 1e-9) / 1e6:8.1f} GB/s")
-    # kernel classes over the whole timed region (decode-shaped + prompt-chunk launches)
-    prof = {k: tuple(a + b for a, b in zip(raw[k], raw[k + "_pf"])) for k in ("q4k_mm", "attention", "step")}
-
-    # dominant kernel class by device time
-    dom = max(("q4k_mm", "attention"), key=lambda k: prof[k][0])
-    ms, by, n = prof[dom]
+    # roofline: the dominant kernel class of the decode steps by device time
+    # (decode-shaped Q4_K matmuls vs decode attention)
+    dom = max(("q4k_mm", "attention"), key=lambda k: raw[k][0])
+    ms, by, n = raw[dom]
     achieved = by / (ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "kernel": "q4k_mm_kernel" if dom == "q4k_mm" else "attn_chunk_kernel+attn_merge_kernel",
+    kname = "q4k_dec_kernel" if dom == "q4k_mm" else "attn_dec_kernel+attn_merge_kernel"
+    roofline = {"bound": "hbm", "kernel": kname,
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kname),
                 "launches": n, "avg_launch_us": round(ms * 1e3 / max(n, 1), 2),
                 "algorithmic_bytes_per_launch": round(by / max(n, 1))}
     other = "attention" if dom == "q4k_mm" else "q4k_mm"
-    oms, oby, on = prof[other]
-    step_ms, _, step_n = prof["step"]
+    oms, oby, on = raw[other]
+    step_ms, _, step_n = raw["step"]
+    pf_ms, pf_by, pf_n = raw["q4k_mm_pf"]
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
@@ -188,8 +203,12 @@ def main():
                    "mixed_prefill_steps": mixed_steps, "arrivals": wl.arrivals - arrivals0,
                    "mean_context_start": round(float(np.mean(ctx0)), 1)},
         "roofline": roofline,
-        "kernels": {"other_class": other, f"{other}_GBs": round(oby / max(oms, 1e-9) / 1e6, 1),
-                    f"{other}_ms": round(oms, 2), "device_step_ms": round(step_ms / max(step_n, 1), 3)},
+        "kernels": {"other_decode_class": other, f"{other}_GBs": round(oby / max(oms, 1e-9) / 1e6, 1),
+                    f"{other}_ms": round(oms, 2),
+                    "decode_step_device_ms": round(step_ms / max(step_n, 1), 3),
+                    "decode_step_median_ms": round(1e3 * float(np.median(dec_s)), 3) if dec_s else None,
+                    "mixed_step_ms": [round(1e3 * t, 1) for t in mix_s],
+                    "prefill_q4k_ms": round(pf_ms, 2), "prefill_q4k_launches": pf_n},
     }
     if not args.no_cpu:
         try:
@@ -198,6 +217,19 @@ def main():
             result["cpu_baseline"] = {"error": str(e)}
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (profiles/q4k_dec_traffic.txt: FETCH_SIZE + WRITE_SIZE per dispatch,
+    scaled by a copy kernel of known size), or None when there is none."""
+    path = os.path.join(ROOT, "profiles", "q4k_dec_traffic.txt")
+    if kernel != "q4k_dec_kernel" or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return round(float(line.split(":", 1)[1]))
+    return None
 
 
 def cpu_baseline_and_parity(m, shape, wl):

@@ -361,8 +361,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
-// Prefill kernel (several 16-row activation tiles).  A workgroup of four
-// waves owns 4R weight tiles of one tensor, NT activation tiles and one split
+// Prefill kernel (several 16-row activation tiles).  A workgroup of WAVES
+// waves owns WAVES*R weight tiles of one tensor, NT activation tiles and one split
 // of super-blocks.  Per block, the NT tiles' activation units are copied into
 // one of two LDS buffers by direct global->LDS loads (issued a block ahead,
 // before the weight prefetch, so waiting for them leaves the weights in
@@ -370,8 +370,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // against all NT activation tiles.  W and frag are not __restrict__: loads
 // through restrict pointers count as invariant and may be moved across the
 // barriers that order them here.
-template <int R, int NT, bool TILED>
-__global__ __launch_bounds__(256) void q4k_pf_kernel(const uint8_t* W, int M, const uint4* frag, int act_tiles,
+template <int R, int NT, bool TILED, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(const uint8_t* W, int M, const uint4* frag, int act_tiles,
                                                      float* __restrict__ out, int64_t ldo,
                                                      int64_t split_stride, int nblk, int bps) {
     __shared__ uint4 s_act[2 * NT * ACT_FRAG_UNITS];
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(256) void q4k_pf_kernel(const uint8_t* W, int M, co
     const int g = lane >> 4;
     const int wv = tid >> 6;
     const int tiles = (M + 15) / 16;
-    const int tile0 = (blockIdx.x * 4 + wv) * R;
+    const int tile0 = (blockIdx.x * WAVES + wv) * R;
     const bool active = tile0 < tiles;
     const int at0 = blockIdx.z * NT;
     const int kb0 = blockIdx.y * bps;
@@ -400,7 +400,7 @@ __global__ __launch_bounds__(256) void q4k_pf_kernel(const uint8_t* W, int M, co
     // copy block kb of activation tiles at0 .. at0+NT-1 (clamped) into `dst`
     // (every address stays inside the operand buffer: at < act_tiles, kb < nblk)
     auto stage = [&](uint4* dst, int kb) {
-        for (int c = wv; c < CHUNKS; c += 4) {
+        for (int c = wv; c < CHUNKS; c += WAVES) {
             const int n = c / (ACT_FRAG_UNITS / 64);
             const int u = (c - n * (ACT_FRAG_UNITS / 64)) * 64;
             const int at = min(at0 + n, act_tiles - 1);
@@ -510,15 +510,15 @@ static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t
                        nblk, bps);
 }
 
-constexpr int PF_R = 2;
+constexpr int PF_R = 2, PF_WAVES = 8;
 
-template <int NT, bool TILED>
+template <int NT, bool TILED, int R = PF_R, int WAVES = PF_WAVES>
 static void launch_pf(const Q4kTarget& t, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk, int bps,
                       int nsplit, hipStream_t s) {
     const int tiles = (t.M + 15) / 16;
     const int act_tiles = a.rows_pad / 16;
-    dim3 grid((tiles + 4 * PF_R - 1) / (4 * PF_R), nsplit, (act_tiles + NT - 1) / NT);
-    hipLaunchKernelGGL((q4k_pf_kernel<PF_R, NT, TILED>), grid, dim3(256), 0, s, (const uint8_t*)t.w, t.M,
+    dim3 grid((tiles + WAVES * R - 1) / (WAVES * R), nsplit, (act_tiles + NT - 1) / NT);
+    hipLaunchKernelGGL((q4k_pf_kernel<R, NT, TILED, WAVES>), grid, dim3(64 * WAVES), 0, s, (const uint8_t*)t.w, t.M,
                        (const uint4*)a.frag, act_tiles, out + t.col, ldo, ss, nblk, bps);
 }
 
@@ -536,7 +536,7 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         const int NT = act_tiles >= 4 ? 4 : (act_tiles >= 2 ? 2 : 1);
         int wgs = 0;
         for (int i = 0; i < n; ++i)
-            wgs += ((t[i].M + 15) / 16 + 4 * PF_R - 1) / (4 * PF_R) * ((act_tiles + NT - 1) / NT);
+            wgs += ((t[i].M + 15) / 16 + PF_WAVES * PF_R - 1) / (PF_WAVES * PF_R) * ((act_tiles + NT - 1) / NT);
         int S = 1;
         while (S * 2 <= max_splits && S * 2 <= nblk / 2 && wgs * S < pf_target) S *= 2;
         const int bps = (nblk + S - 1) / S;
