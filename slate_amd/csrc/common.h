@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 #include <stddef.h>
 #include <stdlib.h>
@@ -33,6 +34,17 @@ bool device_ok();            // a gfx950 device was opened
 #define SH_REQUIRE(cond, ...)                                                     \
     do {                                                                          \
         if (!(cond)) { ::slate_hip::set_error(-1, __VA_ARGS__); return -1; }      \
+    } while (0)
+
+// Kernel launch that, when timing events are given, has the dispatch itself
+// record them at kernel start / end (hipExtLaunchKernelGGL), so the elapsed
+// time is the kernel's own duration without the gaps around it.
+#define SH_LAUNCH(ev0, ev1, kernel, grid, block, shmem, stream, ...)                                \
+    do {                                                                                          \
+        if ((ev0) != nullptr || (ev1) != nullptr)                                                 \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, ev0, ev1, 0, __VA_ARGS__);   \
+        else                                                                                      \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                  \
     } while (0)
 
 // Scratch owned by the backend: grown on demand, reused across calls.  Every
@@ -78,8 +90,11 @@ struct Q4kTargets {                 // kernel-argument form
     int grp0[3];                    // first wave group of each tensor
     int n, grp_end;
 };
+// ev_start / ev_stop (optional) are recorded at the start of the first and
+// the end of the last kernel of the matmul.
 int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo,
-               int64_t split_stride, int max_splits, int* S_out, hipStream_t s);
+               int64_t split_stride, int max_splits, int* S_out, hipStream_t s,
+               hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 // TILED weight layout (16-row tiles, see k_q4k.hip).
 size_t q4k_tiled_bytes(int M, int K);
 int launch_q4k_tile(void* dst, const void* src, int M, int K, hipStream_t s);

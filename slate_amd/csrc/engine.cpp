@@ -66,6 +66,8 @@ struct slate_hip_llama {
     float *xlast = nullptr, *logits = nullptr;
     float* part = nullptr;
     size_t part_floats = 0;
+    float* ssq = nullptr;          // [T_pad][D/256] block sums of squares (deferred RMSNorm)
+    bool defer_norm = true;
     float *att_po = nullptr, *att_pml = nullptr;
     Act16 act{};
     int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
@@ -169,6 +171,8 @@ int alloc_runtime(slate_hip_llama* m) {
     char* fr = nullptr;
     if (dalloc(m, &fr, act_frag_bytes((int)T, Kmax))) return -2;
     m->act = Act16{fr, 0, (int)T, Kmax};
+    if (dalloc(m, &m->ssq, T * (D / QK + 1))) return -2;
+    m->defer_norm = getenv("SLATE_HIP_FUSED_NORM") == nullptr || atoi(getenv("SLATE_HIP_FUSED_NORM")) != 0;
     const int S = m->max_slots;
     const size_t in_ints = 3 * (size_t)S + 4 * T;
     if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
@@ -284,16 +288,24 @@ int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int 
     return tile_lin(m, l, row);
 }
 
-// Profiling: events recorded on the stream around launches of a class
-// (0 = Q4_K matmul, 1 = attention, 2 = whole step) with the launch's
-// algorithmic bytes; folded into the totals after the step's sync.
-size_t prof_mark(slate_hip_llama* m, hipStream_t s) {
+// Profiling: event pairs around launches of a kernel class (see the header)
+// with the launch's algorithmic bytes; folded into the totals after the
+// step's sync.  Kernel classes get events recorded by the dispatches
+// themselves (prof_event + SH_LAUNCH), steps get stream events (prof_mark).
+size_t prof_event(slate_hip_llama* m) {
     if (m->prof_used == m->prof_ev.size()) {
         hipEvent_t e;
         if (hipEventCreate(&e) != hipSuccess) return (size_t)-1;
         m->prof_ev.push_back(e);
     }
-    size_t i = m->prof_used++;
+    return m->prof_used++;
+}
+
+hipEvent_t prof_ev(slate_hip_llama* m, size_t i) { return i == (size_t)-1 ? nullptr : m->prof_ev[i]; }
+
+size_t prof_mark(slate_hip_llama* m, hipStream_t s) {
+    size_t i = prof_event(m);
+    if (i == (size_t)-1) return i;
     if (hipEventRecord(m->prof_ev[i], s) != hipSuccess) return (size_t)-1;
     return i;
 }
@@ -330,6 +342,12 @@ Act16 act_for(slate_hip_llama* m, int T, int K) {
     return a;
 }
 
+// RMSNorm whose row factor is applied by the consumer of the group's matmul
+// (residual_act + RowNorm): only for all-Q4_K groups of width % 256 == 0.
+bool defer_norm(const slate_hip_llama* m, const GroupIn& gi, int D) {
+    return m->defer_norm && gi.q4 && !gi.f32 && D % QK == 0;
+}
+
 // One matmul group: the linears in `lins` read the same input (operand `a`
 // for Q4_K, rows X [T, K] for f32) and write column ranges of one partial
 // buffer [S][T_pad][ldo]; *S_out = S.
@@ -350,10 +368,10 @@ int mm_group(slate_hip_llama* m, const Act16* a, const float* X, int T, int K, c
                 t[nq++] = Q4kTarget{lins[i]->w, lins[i]->M, col[i]};
                 bytes += (double)lins[i]->bytes() + 4.0 * T * lins[i]->M;
             }
-        size_t e0 = m->prof_on ? prof_mark(m, s) : 0;
-        int rc = launch_q4k(t, nq, true, *a, m->part, ldo, ss, max_splits, &S, s);
+        const size_t e0 = m->prof_on ? prof_event(m) : (size_t)-1, e1 = m->prof_on ? prof_event(m) : (size_t)-1;
+        int rc = launch_q4k(t, nq, true, *a, m->part, ldo, ss, max_splits, &S, s, prof_ev(m, e0), prof_ev(m, e1));
         if (rc) return rc;
-        if (m->prof_on) m->prof_recs.push_back({tpad == 16 ? 0 : 3, bytes, e0, prof_mark(m, s)});
+        if (m->prof_on) m->prof_recs.push_back({tpad == 16 ? 0 : 3, bytes, e0, e1});
     }
     for (int i = 0; i < nl; ++i) {
         const Lin& l = *lins[i];
@@ -376,13 +394,13 @@ int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
         a.K = c.d_model;
         int rc = launch_act16_from_f32(a, m->xlast, c.d_model, s);
         if (rc) return rc;
-        size_t e0 = m->prof_on ? prof_mark(m, s) : 0;
+        const size_t e0 = m->prof_on ? prof_event(m) : (size_t)-1, e1 = m->prof_on ? prof_event(m) : (size_t)-1;
         Q4kTarget t{l.w, c.vocab, 0};
         int S = 1;
-        rc = launch_q4k(&t, 1, true, a, m->logits, c.vocab, 0, 1, &S, s);
+        rc = launch_q4k(&t, 1, true, a, m->logits, c.vocab, 0, 1, &S, s, prof_ev(m, e0), prof_ev(m, e1));
         if (m->prof_on)
             m->prof_recs.push_back({a.rows_pad == 16 ? 0 : 3, (double)l.bytes() + 4.0 * n * (c.d_model + c.vocab), e0,
-                                    prof_mark(m, s)});
+                                    e1});
         return rc;
     }
     return launch_mm_f32(m->logits, m->xlast, (const float*)l.w, n, c.vocab, c.d_model, c.vocab, s);
@@ -403,6 +421,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
     const int tpad = row_pad(T);
     int S_prev = 0;
+    RowNorm rn{};
     for (int li = 0; li < c.n_layers; ++li) {
         const LayerDev& Ld = m->L[li];
         int S;
@@ -412,31 +431,38 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             int64_t col[3] = {0, D, D + kvd};
             const GroupIn gi = group_in(g, 3);
             Act16 a = act_for(m, T, D);
-            if ((rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, li ? m->part : nullptr, S_prev,
-                                         (int64_t)tpad * D, Ld.attn_norm, T, D, c.rms_eps, gi.q4 ? &a : nullptr, s)))
-                return rc;
+            rn = RowNorm{nullptr, 0, D, c.rms_eps};
+            if (defer_norm(m, gi, D)) {   // all-Q4_K group: norm factor applied by rope_kv
+                rn.ssq = m->ssq;
+                rn.nblk = D / QK;
+                rc = launch_residual_act(m->x, li ? m->part : nullptr, S_prev, (int64_t)tpad * D, Ld.attn_norm, T, D,
+                                         a, m->ssq, s);
+            } else {
+                rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, li ? m->part : nullptr, S_prev,
+                                        (int64_t)tpad * D, Ld.attn_norm, T, D, c.rms_eps, gi.q4 ? &a : nullptr, s);
+            }
+            if (rc) return rc;
             if ((rc = mm_group(m, &a, m->xn, T, D, g, col, 3, D + 2 * kvd, &S, s))) return rc;
         }
         float* Kl = m->Kpool + (int64_t)li * m->layer_stride;
         float* Vl = m->Vpool + (int64_t)li * m->layer_stride;
         if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd, m->tok2seq,
                                  m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd, m->head_stride, m->rope_cs,
-                                 s)))
+                                 rn, s)))
             return rc;
         {
             const Lin* g[1] = {&Ld.o};
             int64_t col[1] = {0};
             const GroupIn gi = group_in(g, 1);
             Act16 a = act_for(m, T, D);
-            size_t ea = m->prof_on ? prof_mark(m, s) : 0;
+            const size_t ea = m->prof_on ? prof_event(m) : (size_t)-1, eb = m->prof_on ? prof_event(m) : (size_t)-1;
             if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
                                               m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
                                               c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
-                                              m->att_pml, gi.q4 ? &a : nullptr, s)))
+                                              m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea), prof_ev(m, eb))))
                 return rc;
             if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
-                m->prof_recs.push_back(
-                    {m->n_pre ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, prof_mark(m, s)});
+                m->prof_recs.push_back({m->n_pre ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, eb});
             if ((rc = mm_group(m, &a, m->att, T, D, g, col, 1, D, &S, s))) return rc;
         }
         {
@@ -444,9 +470,16 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             int64_t col[2] = {0, H};
             const GroupIn gi = group_in(g, 2);
             Act16 a = act_for(m, T, D);
-            if ((rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm,
-                                         T, D, c.rms_eps, gi.q4 ? &a : nullptr, s)))
-                return rc;
+            rn = RowNorm{nullptr, 0, D, c.rms_eps};
+            if (defer_norm(m, gi, D)) {   // all-Q4_K group: norm factor applied by silu_act
+                rn.ssq = m->ssq;
+                rn.nblk = D / QK;
+                rc = launch_residual_act(m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm, T, D, a, m->ssq, s);
+            } else {
+                rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm,
+                                        T, D, c.rms_eps, gi.q4 ? &a : nullptr, s);
+            }
+            if (rc) return rc;
             if ((rc = mm_group(m, &a, m->xn, T, D, g, col, 2, 2 * H, &S, s))) return rc;
         }
         {
@@ -456,8 +489,8 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             Act16 a = act_for(m, T, H);
             if (H % QK == 0)
                 rc = launch_silu_act(gi.f32 ? m->h : nullptr, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H,
-                                     2 * H, gi.q4 ? &a : nullptr, s);
-            else   // no Q4_K operand exists for this width
+                                     2 * H, gi.q4 ? &a : nullptr, rn, s);
+            else   // no Q4_K operand exists for this width (and no deferred norm: gate/up are f32)
                 rc = launch_silu_mul(m->h, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H, 2 * H, 2 * H, s);
             if (rc) return rc;
             if ((rc = mm_group(m, &a, m->h, T, H, g, col, 1, D, &S, s))) return rc;

@@ -347,11 +347,12 @@ struct AttnArgs {
     int64_t head_stride;
     int nch_max;
     float *po, *pml;
+    hipEvent_t ev0;    // recorded at the start of the first attention kernel (optional)
 };
 
 template <int HD, int G, int QB>
 static void launch_blk(dim3 grid, hipStream_t s, const AttnArgs& a) {
-    hipLaunchKernelGGL((attn_block_kernel<HD, G, QB>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,
+    SH_LAUNCH(a.ev0, nullptr, (attn_block_kernel<HD, G, QB>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,
                        a.qn, a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);
 }
 
@@ -386,7 +387,8 @@ static int launch_dec_hd(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
     switch (G) {
 #define SH_DEC(GG)                                                                                            \
     case GG:                                                                                                  \
-        hipLaunchKernelGGL((attn_dec_kernel<HD, GG>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,  \
+        SH_LAUNCH(a.ev0, nullptr, (attn_dec_kernel<HD, GG>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp,  \
+                  a.qt0,                                                                                      \
                            a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);    \
         return 0;
         SH_DEC(1) SH_DEC(2) SH_DEC(4) SH_DEC(8)
@@ -399,7 +401,7 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                            hipStream_t s) {
+                            hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop) {
     if (T <= 0) return 0;
     if (Hkv <= 0 || Hq % Hkv != 0) {
         set_error(-1, "attention: n_q_heads %d not a multiple of n_kv_heads %d", Hq, Hkv);
@@ -411,7 +413,7 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
     }
     const int G = Hq / Hkv;
     const int nch_max = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
-    AttnArgs a{q, Kp, Vp, nullptr, nullptr, tok2seq, tok_pos, kv_base, Hq, head_stride, nch_max, po, pml};
+    AttnArgs a{q, Kp, Vp, nullptr, nullptr, tok2seq, tok_pos, kv_base, Hq, head_stride, nch_max, po, pml, ev_start};
     for (int pass = 0; pass < 2; ++pass) {
         const bool prefill = pass == 1;
         const int nblk = prefill ? n_pre : n_dec;
@@ -437,11 +439,12 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
             return rc;
         }
         SH_CHECK_LAUNCH();
+        a.ev0 = nullptr;                           // only the first kernel records the start
     }
     const int nb = (Hq * HD + 255) / 256;
     dim3 mgrid((nb + 3) / 4, act ? act->rows_pad : T);
-    hipLaunchKernelGGL(attn_merge_kernel, mgrid, dim3(256), 0, s, out, po, pml, tok_pos, T, Hq, HD, nch_max,
-                       act ? *act : Act16{}, act ? 1 : 0);
+    SH_LAUNCH(nullptr, ev_stop, attn_merge_kernel, mgrid, dim3(256), 0, s, out, po, pml, tok_pos, T, Hq, HD, nch_max,
+              act ? *act : Act16{}, act ? 1 : 0);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -452,7 +455,7 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
                             int Hq, int Hkv, int HD, int64_t head_stride, int max_pos, float* po,
                             float* pml, hipStream_t s) {
     return launch_attention_blocks(out, q, Kp, Vp, tok2seq, tok_pos, kv_base, T, nullptr, T, nullptr, nullptr, 0,
-                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s);
+                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s, nullptr, nullptr);
 }
 
 // ---------------------------------------------------------------------------

@@ -504,26 +504,26 @@ static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, i
 
 template <int R, bool TILED>
 static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk,
-                       int bps, int nsplit, hipStream_t s) {
+                       int bps, int nsplit, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     dim3 grid((tg.grp_end + 3) / 4, nsplit);
-    hipLaunchKernelGGL((q4k_dec_kernel<R, TILED>), grid, dim3(256), 0, s, tg, (const uint4*)a.frag, out, ldo, ss,
-                       nblk, bps);
+    SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED>), grid, dim3(256), 0, s, tg, (const uint4*)a.frag, out, ldo, ss,
+              nblk, bps);
 }
 
 constexpr int PF_R = 2, PF_WAVES = 8;
 
 template <int NT, bool TILED, int R = PF_R, int WAVES = PF_WAVES>
 static void launch_pf(const Q4kTarget& t, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk, int bps,
-                      int nsplit, hipStream_t s) {
+                      int nsplit, hipStream_t s, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
     const int tiles = (t.M + 15) / 16;
     const int act_tiles = a.rows_pad / 16;
     dim3 grid((tiles + WAVES * R - 1) / (WAVES * R), nsplit, (act_tiles + NT - 1) / NT);
-    hipLaunchKernelGGL((q4k_pf_kernel<R, NT, TILED, WAVES>), grid, dim3(64 * WAVES), 0, s, (const uint8_t*)t.w, t.M,
-                       (const uint4*)a.frag, act_tiles, out + t.col, ldo, ss, nblk, bps);
+    SH_LAUNCH(e0, e1, (q4k_pf_kernel<R, NT, TILED, WAVES>), grid, dim3(64 * WAVES), 0, s, (const uint8_t*)t.w, t.M,
+              (const uint4*)a.frag, act_tiles, out + t.col, ldo, ss, nblk, bps);
 }
 
 int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo, int64_t split_stride,
-               int max_splits, int* S_out, hipStream_t s) {
+               int max_splits, int* S_out, hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop) {
     if (n < 1 || n > 3) { set_error(-1, "q4k: 1..3 fused tensors"); return -1; }
     const int nblk = a.K / QK;
     if (nblk < 1) { set_error(-1, "q4k: K=%d", a.K); return -1; }
@@ -542,12 +542,13 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         const int bps = (nblk + S - 1) / S;
         S = (nblk + bps - 1) / bps;
         for (int i = 0; i < n; ++i) {
+            hipEvent_t e0 = i == 0 ? ev_start : nullptr, e1 = i == n - 1 ? ev_stop : nullptr;
             if (NT == 4) {
-                if (tiled) launch_pf<4, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
-                else launch_pf<4, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
+                if (tiled) launch_pf<4, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
+                else launch_pf<4, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
             } else {
-                if (tiled) launch_pf<2, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
-                else launch_pf<2, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s);
+                if (tiled) launch_pf<2, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
+                else launch_pf<2, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
             }
         }
         SH_CHECK_LAUNCH();
@@ -572,13 +573,13 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
     tg.n = n;
     tg.grp_end = grp;
     if (tiled) {
-        if (R == 4) launch_dec<4, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
-        else if (R == 2) launch_dec<2, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
-        else launch_dec<1, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+        if (R == 4) launch_dec<4, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+        else if (R == 2) launch_dec<2, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+        else launch_dec<1, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
     } else {
-        if (R == 4) launch_dec<4, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
-        else if (R == 2) launch_dec<2, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
-        else launch_dec<1, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s);
+        if (R == 4) launch_dec<4, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+        else if (R == 2) launch_dec<2, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+        else launch_dec<1, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
     }
     SH_CHECK_LAUNCH();
     *S_out = S;

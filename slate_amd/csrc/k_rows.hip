@@ -167,37 +167,96 @@ int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int 
 // (act16.h), so a split-K sum, the row operation and the operand conversion
 // are one pass over the row.
 
-// sum_{k < n} p[k * stride] in split order, loads issued eight at a time so
-// the latency of the partials is paid once per batch, not once per split.
+// sum_{k < n} p[k * stride] in split order (n >= 1), loads issued eight at a
+// time (clamped, so every address is a valid partial) and added under a
+// predicate, so the latency of the partials is paid once per eight splits.
 __device__ __forceinline__ float4 split_sum4(const float* p, int n, int64_t stride) {
-    float4 s = *(const float4*)p;
-    int k = 1;
-    for (; k + 8 <= n; k += 8) {
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < n; k += 8) {
         float4 t[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = *(const float4*)(p + (int64_t)(k + i) * stride);
+        for (int i = 0; i < 8; ++i) t[i] = *(const float4*)(p + (int64_t)min(k + i, n - 1) * stride);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { s.x += t[i].x; s.y += t[i].y; s.z += t[i].z; s.w += t[i].w; }
-    }
-    for (; k < n; ++k) {
-        const float4 t = *(const float4*)(p + (int64_t)k * stride);
-        s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+        for (int i = 0; i < 8; ++i)
+            if (k + i < n) { s.x += t[i].x; s.y += t[i].y; s.z += t[i].z; s.w += t[i].w; }
     }
     return s;
 }
 
 __device__ __forceinline__ float split_sum1(const float* p, int n, int64_t stride) {
-    float s = p[0];
-    int k = 1;
-    for (; k + 8 <= n; k += 8) {
+    float s = 0.f;
+    for (int k = 0; k < n; k += 8) {
         float t[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = p[(int64_t)(k + i) * stride];
+        for (int i = 0; i < 8; ++i) t[i] = p[(int64_t)min(k + i, n - 1) * stride];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += t[i];
+        for (int i = 0; i < 8; ++i)
+            if (k + i < n) s += t[i];
     }
-    for (; k < n; ++k) s += p[(int64_t)k * stride];
     return s;
+}
+
+// RMSNorm factor of row r from the per-256-block sums of squares that
+// residual_act_kernel leaves: inv = 1/sqrtf((float)(sum x^2 / D) + eps)
+// (backend_cpu.c:48-76; block sums added in double, in block order).
+__device__ __forceinline__ float row_inv_rms(const float* ssq, int r, int nblk, int D, float eps) {
+    double sq = 0.0;
+    for (int kb = 0; kb < nblk; ++kb) sq += (double)ssq[(size_t)r * nblk + kb];
+    return 1.0f / sqrtf((float)(sq / (double)D) + eps);
+}
+
+// Residual + RMSNorm split across the whole chip (all-Q4_K consumers): one
+// wave per 256-element block of a row does x += sum_s delta[s] (fixed split
+// order, written back), stores the block's sum of squares in
+// ssq[r * D/256 + kb] and emits x * w (without the row factor) as the Q4_K
+// operand.  The consumer of the matmul that follows multiplies each row by
+// row_inv_rms() (the matmul is linear in each row), so no kernel has to wait
+// for a whole row.  Rows >= rows write zero operand rows.
+__global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x, const float* __restrict__ delta,
+                                                           int nsplit, int64_t split_stride,
+                                                           const float* __restrict__ w, int rows, int D, Act16 a,
+                                                           float* __restrict__ ssq) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nblk = D / QK;
+    if (kb >= nblk) return;                       // whole wave
+    const int r = blockIdx.y;
+    const int e = kb * QK + 4 * lane;
+    float4 yv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < rows) {
+        float* xr = x + (size_t)r * D + e;
+        float4 xv = *(const float4*)xr;
+        if (delta) {
+            const float4 sm = split_sum4(delta + (size_t)r * D + e, nsplit, split_stride);
+            xv.x += sm.x; xv.y += sm.y; xv.z += sm.z; xv.w += sm.w;
+            *(float4*)xr = xv;
+        }
+        float sq = 0.f;
+        sq = __builtin_fmaf(xv.x, xv.x, sq);
+        sq = __builtin_fmaf(xv.y, xv.y, sq);
+        sq = __builtin_fmaf(xv.z, xv.z, sq);
+        sq = __builtin_fmaf(xv.w, xv.w, sq);
+        for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+        if (lane == 0) ssq[(size_t)r * nblk + kb] = sq;
+        const float4 wv = *(const float4*)(w + e);
+        yv = make_float4(xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w);
+    }
+    act16_store_block(a, r, kb, lane, yv);
+}
+
+int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_stride, const float* w, int rows,
+                        int D, const Act16& a, float* ssq, hipStream_t s) {
+    if (rows <= 0) return 0;
+    if (D % QK || a.K != D) {
+        set_error(-1, "residual_act: width %d is not a multiple of 256", D);
+        return -1;
+    }
+    const int nblk = D / QK;
+    hipLaunchKernelGGL(residual_act_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, x, delta, nsplit,
+                       split_stride, w, rows, D, a, ssq);
+    SH_CHECK_LAUNCH();
+    return 0;
 }
 
 // Residual + RMSNorm: x += sum_s delta[s] (fixed split order, written back),
@@ -283,7 +342,8 @@ int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64
 // One wave per 256-element block of a row (H % 256 == 0).
 __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, const float* __restrict__ gate,
                                                        const float* __restrict__ up, int rows, int H, int nsplit,
-                                                       int64_t split_stride, int64_t ld, Act16 a, int act) {
+                                                       int64_t split_stride, int64_t ld, Act16 a, int act,
+                                                       RowNorm rn) {
     const int lane = threadIdx.x & 63;
     const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (kb * QK >= H) return;                     // whole wave
@@ -293,7 +353,12 @@ __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, co
     if (r < rows) {
         const float* gp = gate + (size_t)r * ld + e;
         const float* upp = up + (size_t)r * ld + e;
-        const float4 g = split_sum4(gp, nsplit, split_stride), u = split_sum4(upp, nsplit, split_stride);
+        float4 g = split_sum4(gp, nsplit, split_stride), u = split_sum4(upp, nsplit, split_stride);
+        if (rn.ssq) {   // gate and up are linear in the normalised row
+            const float inv = row_inv_rms(rn.ssq, r, rn.nblk, rn.D, rn.eps);
+            g = make_float4(g.x * inv, g.y * inv, g.z * inv, g.w * inv);
+            u = make_float4(u.x * inv, u.y * inv, u.z * inv, u.w * inv);
+        }
         h = make_float4((g.x / (1.0f + expf(-g.x))) * u.x, (g.y / (1.0f + expf(-g.y))) * u.y,
                         (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
         if (y) *(float4*)(y + (size_t)r * H + e) = h;
@@ -302,7 +367,7 @@ __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, co
 }
 
 int launch_silu_act(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
-                    int64_t split_stride, int64_t ld, const Act16* a, hipStream_t s) {
+                    int64_t split_stride, int64_t ld, const Act16* a, const RowNorm& rn, hipStream_t s) {
     if (rows <= 0) return 0;
     if (H % QK || (a && a->K != H)) {
         set_error(-1, "silu_act: width %d is not a multiple of 256", H);
@@ -311,7 +376,7 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
     const int nblk = H / QK;
     dim3 grid((nblk + 3) / 4, a ? a->rows_pad : rows);
     hipLaunchKernelGGL(silu_act_kernel, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride, ld,
-                       a ? *a : Act16{}, a ? 1 : 0);
+                       a ? *a : Act16{}, a ? 1 : 0, rn);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -326,7 +391,7 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, f
                                                      const int32_t* __restrict__ tok_pos,
                                                      const int64_t* __restrict__ kv_base, int n_heads,
                                                      int n_kv_heads, int hd, int64_t head_stride,
-                                                     const float* __restrict__ cs) {
+                                                     const float* __restrict__ cs, RowNorm rn) {
 #pragma clang fp contract(off)
     const int u = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int D = n_heads * hd, kvd = n_kv_heads * hd, half = hd / 2;
@@ -334,7 +399,12 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, f
     const int ap = p < 0 ? -p : p;
     const float sg = p < 0 ? -1.0f : 1.0f;
     const float* pr = part + (size_t)t * qkv_ld;
-    auto col = [&](int c) { return split_sum1(pr + c, nsplit, split_stride); };
+    // q, k, v are linear in the normalised row: apply its RMSNorm factor here
+    const float inv = rn.ssq ? row_inv_rms(rn.ssq, t, rn.nblk, rn.D, rn.eps) : 1.0f;
+    auto col = [&](int c) {
+        const float v = split_sum1(pr + c, nsplit, split_stride);
+        return rn.ssq ? v * inv : v;
+    };
     if (u < n_heads) {
         for (int i = lane; i < half; i += 64) {
             const int c0 = u * hd + i;
@@ -362,11 +432,12 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, f
 
 int launch_rope_kv(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit, int64_t split_stride,
                    int qkv_ld, const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
-                   int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, hipStream_t s) {
+                   int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, const RowNorm& rn,
+                   hipStream_t s) {
     if (T <= 0) return 0;
     hipLaunchKernelGGL(rope_kv_kernel, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout, Kpool, Vpool, part,
                        nsplit, split_stride, qkv_ld, tok2seq, tok_pos, kv_base, n_heads, n_kv_heads, hd,
-                       head_stride, cs);
+                       head_stride, cs, rn);
     SH_CHECK_LAUNCH();
     return 0;
 }

@@ -16,15 +16,27 @@ int launch_add(float* y, const float* x, int64_t n, hipStream_t s);
 int launch_embed_rows(float* y, const float* W, const int32_t* tok, int T, int V, int D, hipStream_t s);
 int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int hd, const float* cs,
                      int max_pos, int* bad, hipStream_t s);
+// Per-row RMSNorm factor deferred to the consumer of a matmul: ssq holds
+// the sums of squares per 256-element block [rows][D/256] (nullptr = none).
+struct RowNorm {
+    const float* ssq;
+    int nblk, D;
+    float eps;
+};
 // Fused engine epilogues; `a` (nullable) receives the Q4_K activation operand
 // of rows_pad rows (rows past `rows` zero), y (nullable) the f32 rows.
 int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64_t split_stride, const float* w,
                        int rows, int D, float eps, const Act16* a, hipStream_t s);
 int launch_silu_act(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
-                    int64_t split_stride, int64_t ld, const Act16* a, hipStream_t s);
+                    int64_t split_stride, int64_t ld, const Act16* a, const RowNorm& rn, hipStream_t s);
 int launch_rope_kv(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit, int64_t split_stride,
                    int qkv_ld, const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
-                   int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, hipStream_t s);
+                   int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, const RowNorm& rn,
+                   hipStream_t s);
+// x += sum of split partials, per-block sums of squares into ssq, x * w as
+// the Q4_K operand (the row factor is left to the consumer, RowNorm).
+int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_stride, const float* w, int rows,
+                        int D, const Act16& a, float* ssq, hipStream_t s);
 int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, hipStream_t s);
 int launch_pack_batch(const int32_t* slot, const int32_t* pos0, const int32_t* n_new, int B, int max_seq,
                       int64_t slot_stride, int T_cap, int32_t* tok_off, int32_t* tok2seq,
@@ -44,7 +56,7 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                            hipStream_t s);
+                            hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
 int launch_attention_ragged(float* out, const float* q, const float* Kp, const float* Vp,
                             const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,

@@ -177,3 +177,28 @@ def test_synthetic_q4k_engine_runs_and_is_batch_invariant():
         assert rc == 0 and rc2 == 0
         assert relerr(l2, lg[2]) < 1e-5
         toks = list(nxt)
+
+
+def test_deferred_rmsnorm_matches_row_rmsnorm(golden, monkeypatch):
+    """The all-Q4_K layers apply the RMSNorm row factor after the matmul
+    (residual_act + the consumer's row scale); the engine built with the
+    whole-row RMSNorm kernel instead gives the same logits to 1e-5 on a
+    ragged batch with a prompt chunk."""
+    t = make_llama(Q4, Q4_SEED, quant="q4k", output_quant="f32")
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("SLATE_HIP_FUSED_NORM", flag)
+        m = slate_amd.Llama.from_tensors(Q4, t, max_slots=3, max_tokens=48)
+        ss = [m.session() for _ in range(3)]
+        rng = np.random.default_rng(11)
+        toks = rng.integers(0, Q4.vocab, 20).astype(np.int32)
+        rc, lg1, nx1 = m.step(ss, [9, 6, 5], toks)
+        assert rc == 0
+        rc, lg2, nx2 = m.step(ss, [1, 1, 7], np.concatenate([nx1[:2], toks[:7]]).astype(np.int32))
+        assert rc == 0
+        outs.append((lg1, lg2))
+        for s in ss:
+            s.free()
+        m.free()
+    for a, b in zip(outs[0], outs[1]):
+        assert relerr(a, b) < 1e-5
