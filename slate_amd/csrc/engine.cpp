@@ -68,6 +68,7 @@ struct slate_hip_llama {
     size_t part_floats = 0;
     float* ssq = nullptr;          // [T_pad][D/256] block sums of squares (deferred RMSNorm)
     bool defer_norm = true;
+    bool tokenwise_attn = false;   // prompt-chunk tokens through the decode attention kernel
     float *att_po = nullptr, *att_pml = nullptr;
     Act16 act{};
     int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
@@ -78,6 +79,7 @@ struct slate_hip_llama {
     // tokens (n_pre)] [prefill block sizes (n_pre)]; d_desc mirrors it.
     int32_t *h_desc = nullptr, *h_tok = nullptr, *h_next = nullptr, *h_status = nullptr;
     int n_dec = 0, n_pre = 0;
+    bool step_mixed = false;       // the step carries a prompt chunk (profiling classes)
     float* h_logits = nullptr;
     std::vector<int> free_slots;
     std::vector<void*> allocs;
@@ -173,6 +175,11 @@ int alloc_runtime(slate_hip_llama* m) {
     m->act = Act16{fr, 0, (int)T, Kmax};
     if (dalloc(m, &m->ssq, T * (D / QK + 1))) return -2;
     m->defer_norm = getenv("SLATE_HIP_FUSED_NORM") == nullptr || atoi(getenv("SLATE_HIP_FUSED_NORM")) != 0;
+    // prompt-chunk tokens attend through the decode kernel (one query token
+    // per work unit, whole coalesced K/V rows; the shared prefix re-reads
+    // hit L2), which beats the query-block kernel for these head sizes
+    m->tokenwise_attn = (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) &&
+                        (getenv("SLATE_HIP_ATTN_TOKENWISE") == nullptr || atoi(getenv("SLATE_HIP_ATTN_TOKENWISE")) != 0);
     const int S = m->max_slots;
     const size_t in_ints = 3 * (size_t)S + 4 * T;
     if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
@@ -462,7 +469,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                                               m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea), prof_ev(m, eb))))
                 return rc;
             if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
-                m->prof_recs.push_back({m->n_pre ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, eb});
+                m->prof_recs.push_back({m->step_mixed ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, eb});
             if ((rc = mm_group(m, &a, m->att, T, D, g, col, 1, D, &S, s))) return rc;
         }
         {
@@ -506,7 +513,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, s))) return rc;
     SH_CHECK_HIP(hipMemcpyAsync(m->h_next, m->next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
     SH_CHECK_HIP(hipMemcpyAsync(m->h_status, m->status, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-    if (m->prof_on) m->prof_recs.push_back({m->n_pre ? 5 : 2, 0.0, estep, prof_mark(m, s)});
+    if (m->prof_on) m->prof_recs.push_back({m->step_mixed ? 5 : 2, 0.0, estep, prof_mark(m, s)});
     if (want_logits)
         SH_CHECK_HIP(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * (size_t)n * c.vocab,
                                     hipMemcpyDeviceToHost, s));
@@ -784,19 +791,19 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
     }
     memcpy(m->h_tok, tokens, sizeof(int32_t) * T);
     // attention work: decode tokens one per block, prompt chunks in blocks of
-    // consecutive tokens of one sequence
+    // consecutive tokens of one sequence (or one block per token, tokenwise)
     {
         const int QB = attn_prefill_block(c.n_heads / c.n_kv_heads);
         int32_t* blk = m->h_tok + T;
         int nd = 0, np = 0, t = 0;
         for (int i = 0; i < n; ++i) {
-            if (n_new[i] == 1) ++nd;
+            if (n_new[i] == 1 || m->tokenwise_attn) nd += n_new[i];
             else np += (n_new[i] + QB - 1) / QB;
         }
         int id = 0, ip = 0;
         for (int i = 0; i < n; ++i) {
-            if (n_new[i] == 1) {
-                blk[id++] = t;
+            if (n_new[i] == 1 || m->tokenwise_attn) {
+                for (int k = 0; k < n_new[i]; ++k) blk[id++] = t + k;
             } else {
                 for (int k = 0; k < n_new[i]; k += QB) {
                     blk[nd + ip] = t + k;
@@ -808,6 +815,7 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
         }
         m->n_dec = nd;
         m->n_pre = np;
+        m->step_mixed = T > n;
     }
     m->step_kv_rows = 0;
     for (int i = 0; i < n; ++i) m->step_kv_rows += (double)sessions[i]->pos + n_new[i];

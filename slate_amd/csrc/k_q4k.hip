@@ -248,26 +248,42 @@ __device__ __forceinline__ void load_act_units(ActOp& A, floatx4& rs, const uint
     rs = floatx4{rv.x, rv.y, rv.z, rv.w};
 }
 
-constexpr int ACT_USED_UNITS = 1092;   // units of a tile-block the kernels read
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt
+// 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+#define SH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+
+// Direct global -> LDS copy of 16 bytes per lane: lane i's bytes land at LDS
+// byte address lds + 16 i (lds wave-uniform).  Issued from inline assembly
+// so the compiler does not treat every later LDS read as waiting on it (its
+// LDS-DMA tracking would stall the weight prefetch too); callers wait with
+// SH_WAIT_VMCNT and a barrier before reading the copied units.
+__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
 
 // Decode kernel (one 16-row activation tile).  A workgroup of four waves
 // owns 4R weight tiles (possibly spread over up to three fused tensors) and
-// one split of super-blocks.  The activation units of a block are staged
-// through a double-buffered LDS tile: in each step the workgroup loads the
-// next block's units (issued first, so waiting for them leaves the weight
-// prefetch in flight) and the next block's weights, computes the current
-// block from LDS, then stores the staged units and meets at one barrier.
+// one split of super-blocks.  The activation units of a block are copied
+// into a double-buffered LDS tile by direct global->LDS loads, one block
+// ahead and issued before the next block's weight loads; each wave holds its
+// R weight tiles in registers, loaded one block ahead; every step ends with
+// one wait for all loads and one barrier.  W and frag are not __restrict__:
+// loads through restrict pointers count as invariant and may be moved across
+// the barriers that order them here.
 template <int R, bool TILED>
-__global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4* __restrict__ frag,
-                                                      float* __restrict__ out, int64_t ldo,
-                                                      int64_t split_stride, int nblk, int bps) {
-    __shared__ uint4 s_act[2][ACT_USED_UNITS];
-    constexpr int NF = (ACT_USED_UNITS + 255) / 256;
+__global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4* frag, float* __restrict__ out,
+                                                      int64_t ldo, int64_t split_stride, int nblk, int bps) {
+    __shared__ uint4 s_act[2 * ACT_FRAG_UNITS];
+    constexpr int CHUNKS = ACT_FRAG_UNITS / 64;       // 1 KiB wave copies per block
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int grp = blockIdx.x * 4 + (tid >> 6);
+    const int wv = tid >> 6;
+    const int grp = blockIdx.x * 4 + wv;
     const int ti = (tg.n > 2 && grp >= tg.grp0[2]) ? 2 : ((tg.n > 1 && grp >= tg.grp0[1]) ? 1 : 0);
     const uint8_t* W = ti == 2 ? tg.w[2] : (ti == 1 ? tg.w[1] : tg.w[0]);
     const int M = ti == 2 ? tg.M[2] : (ti == 1 ? tg.M[1] : tg.M[0]);
@@ -289,46 +305,41 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
         if (TILED) load_wtile_tiled(w, wp[r] + (size_t)kb * (16 * QBLOCK), lane);
         else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
     };
-    uint4 fr[NF];
+    // copy block kb's units (kb < nblk: inside the operand buffer) into dst
+    auto stage = [&](uint4* dst, int kb) {
+        for (int c = wv; c < CHUNKS; c += 4)
+            lds_copy16(frag + (size_t)kb * ACT_FRAG_UNITS + c * 64 + lane,
+                       __builtin_amdgcn_readfirstlane(lds_addr(dst + c * 64)));
+    };
     WTile wc[R], wn[R];
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    {
-        const uint4* f0 = frag + (size_t)kb0 * ACT_FRAG_UNITS;
-#pragma unroll
-        for (int i = 0; i < NF; ++i) fr[i] = f0[min(tid + 256 * i, ACT_USED_UNITS - 1)];
-    }
+    stage(s_act, kb0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
-#pragma unroll
-    for (int i = 0; i < NF; ++i)
-        if (tid + 256 * i < ACT_USED_UNITS) s_act[0][tid + 256 * i] = fr[i];
+    __builtin_amdgcn_sched_barrier(0);
+    SH_WAIT_VMCNT(0);
     __syncthreads();
-
     for (int b = 0; b < nb; ++b) {
-        // unconditional (clamped) prefetch: no branch around a load
+        const uint4* cur = s_act + (b & 1) * ACT_FRAG_UNITS;
         const int kn = kb0 + min(b + 1, nb - 1);
-        const uint4* fn = frag + (size_t)kn * ACT_FRAG_UNITS;
+        if (b + 1 < nb) stage(s_act + ((b + 1) & 1) * ACT_FRAG_UNITS, kn);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < NF; ++i) fr[i] = fn[min(tid + 256 * i, ACT_USED_UNITS - 1)];
-#pragma unroll
-        for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
+        for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);   // unconditional (clamped) prefetch
         __builtin_amdgcn_sched_barrier(0);
         if (active) {
             ActOp A;
             floatx4 rs;
-            load_act_units(A, rs, s_act[b & 1], lane);
+            load_act_units(A, rs, cur, lane);
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] += q4k_mma(q4k_wop(wc[r], g), A, g) * rs;
         }
-        if (b + 1 < nb) {
-            uint4* sn = s_act[(b + 1) & 1];
-#pragma unroll
-            for (int i = 0; i < NF; ++i)
-                if (tid + 256 * i < ACT_USED_UNITS) sn[tid + 256 * i] = fr[i];
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        SH_WAIT_VMCNT(0);                              // next block's units and weights have landed
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < R; ++r) wc[r] = wn[r];
@@ -343,22 +354,6 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
             for (int i = 0; i < 4; ++i) o[(int64_t)(4 * g + i) * ldo + row] = acc[r][i];
         }
     }
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt
-// 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
-#define SH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
-
-// Direct global -> LDS copy of 16 bytes per lane: lane i's bytes land at LDS
-// byte address lds + 16 i (lds wave-uniform).  Issued from inline assembly
-// so the compiler does not treat every later LDS read as waiting on it (its
-// LDS-DMA tracking would stall the weight prefetch too); callers wait with
-// SH_WAIT_VMCNT and a barrier before reading the copied units.
-__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
 // Prefill kernel (several 16-row activation tiles).  A workgroup of WAVES
