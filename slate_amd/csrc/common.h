@@ -78,6 +78,14 @@ int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream
 int launch_sum_splits(float* Y, const float* part, int nsplit, int rows, int rows_pad, int M,
                       hipStream_t s);
 
+// Per-row RMSNorm factor deferred to the consumer of a matmul: ssq holds
+// the sums of squares per 256-element block [rows][D/256] (nullptr = none).
+struct RowNorm {
+    const float* ssq;
+    int nblk, D;
+    float eps;
+};
+
 // Up to three Q4_K tensors sharing one input, fused into one launch; tensor i
 // writes output columns [col, col + M).  Split-K partials: element (split,
 // row b, col m) goes to out[split * split_stride + b * ldo + m] for

@@ -167,50 +167,72 @@ __device__ __forceinline__ float f16_to_f32_hw(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// Dequantised B operand of one weight tile and block: q * sc for the 8 K
-// steps, the sub-block mins, d and 64 * dmin.
-struct WOp { half8_t b[8]; half4_t bmin; float d, dmin64; };
+// Per-block constants of one weight tile for lane group g: the f16 fma
+// terms that turn nibbles into q * sc (low nibble: 1024+q -> (1024+q)*sc -
+// 1024*sc; high nibble: 1024+16q -> ((1024+16q)*sc - 1024*sc)/16), the
+// sub-block mins as the min-term operand, d and 64 * dmin.
+struct WScale { half2_t lm0, lm1, la0, la1, hm0, hm1, ha0, ha1; half4_t bmin; float d, dmin64; };
 
-__device__ __forceinline__ WOp q4k_wop(const WTile& w, int g) {
-    WOp B;
+__device__ __forceinline__ WScale q4k_wscale(const WTile& w, int g) {
+    WScale c;
     ScaleBytes sb = unpack_scales(w.hdr.y, w.hdr.z, w.hdr.w);
     uint32_t scw = g < 2 ? sb.sc_lo : sb.sc_hi;
     int sh = 16 * (g & 1);
     _Float16 s0 = (_Float16)(float)((scw >> sh) & 0xffu);
     _Float16 s1 = (_Float16)(float)((scw >> (sh + 8)) & 0xffu);
-    // q*sc from 1024+q (low nibble) or 1024+16q (high nibble) in one exact fma
-    const half2_t lo_m0 = {s0, s0}, lo_m1 = {s1, s1};
-    const half2_t lo_a0 = lo_m0 * (_Float16)-1024.0f, lo_a1 = lo_m1 * (_Float16)-1024.0f;
-    const half2_t hi_m0 = lo_m0 * (_Float16)0.0625f, hi_m1 = lo_m1 * (_Float16)0.0625f;
-    const half2_t hi_a0 = lo_m0 * (_Float16)-64.0f, hi_a1 = lo_m1 * (_Float16)-64.0f;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        const uint4 Q = t < 4 ? w.qa : w.qb;
-        const int tq = t & 3;
-        const uint32_t mask = (tq & 2) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-        const uint32_t w0 = ((tq & 1) ? Q.z : Q.x) & mask;
-        const uint32_t w1 = ((tq & 1) ? Q.w : Q.y) & mask;
-        const half2_t mul = (tq & 2) ? (t < 4 ? hi_m0 : hi_m1) : (t < 4 ? lo_m0 : lo_m1);
-        const half2_t add = (tq & 2) ? (t < 4 ? hi_a0 : hi_a1) : (t < 4 ? lo_a0 : lo_a1);
-        half2_t p0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u));
-        half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u));
-        half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u));
-        half2_t p3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u));
-        p0 = __builtin_elementwise_fma(p0, mul, add);
-        p1 = __builtin_elementwise_fma(p1, mul, add);
-        p2 = __builtin_elementwise_fma(p2, mul, add);
-        p3 = __builtin_elementwise_fma(p3, mul, add);
-        B.b[t] = half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-    }
+    c.lm0 = half2_t{s0, s0};
+    c.lm1 = half2_t{s1, s1};
+    c.la0 = c.lm0 * (_Float16)-1024.0f;
+    c.la1 = c.lm1 * (_Float16)-1024.0f;
+    c.hm0 = c.lm0 * (_Float16)0.0625f;
+    c.hm1 = c.lm1 * (_Float16)0.0625f;
+    c.ha0 = c.lm0 * (_Float16)-64.0f;
+    c.ha1 = c.lm1 * (_Float16)-64.0f;
     // mins of sub-blocks 4g..4g+3 for g < 2 (groups 2, 3 carry the zero padding
     // on the activation side, so their values do not matter)
     const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const uint32_t mw = (g & 1) ? sb.mn_hi : sb.mn_lo;
     const half2_t m01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) + k1024;
     const half2_t m23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) + k1024;
-    B.bmin = half4_t{m01.x, m01.y, m23.x, m23.y};
-    B.d = f16_to_f32_hw(w.hdr.x & 0xffffu);
-    B.dmin64 = f16_to_f32_hw(w.hdr.x >> 16) * 64.0f;
+    c.bmin = half4_t{m01.x, m01.y, m23.x, m23.y};
+    c.d = f16_to_f32_hw(w.hdr.x & 0xffffu);
+    c.dmin64 = f16_to_f32_hw(w.hdr.x >> 16) * 64.0f;
+    return c;
+}
+
+// B operand of K step t: q * sc exact in f16 (q <= 15, sc <= 63), built from
+// 1024+q (low nibble) or 1024+16q (high nibble) by v_perm and one exact fma.
+__device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int t) {
+    const uint4 Q = t < 4 ? w.qa : w.qb;
+    const int tq = t & 3;
+    const uint32_t mask = (tq & 2) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+    const uint32_t w0 = ((tq & 1) ? Q.z : Q.x) & mask;
+    const uint32_t w1 = ((tq & 1) ? Q.w : Q.y) & mask;
+    const half2_t mul = (tq & 2) ? (t < 4 ? c.hm0 : c.hm1) : (t < 4 ? c.lm0 : c.lm1);
+    const half2_t add = (tq & 2) ? (t < 4 ? c.ha0 : c.ha1) : (t < 4 ? c.la0 : c.la1);
+    half2_t p0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u));
+    half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u));
+    half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u));
+    half2_t p3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u));
+    p0 = __builtin_elementwise_fma(p0, mul, add);
+    p1 = __builtin_elementwise_fma(p1, mul, add);
+    p2 = __builtin_elementwise_fma(p2, mul, add);
+    p3 = __builtin_elementwise_fma(p3, mul, add);
+    return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// Dequantised B operand of one weight tile and block: q * sc for the 8 K
+// steps, the sub-block mins, d and 64 * dmin.
+struct WOp { half8_t b[8]; half4_t bmin; float d, dmin64; };
+
+__device__ __forceinline__ WOp q4k_wop(const WTile& w, int g) {
+    WOp B;
+    const WScale c = q4k_wscale(w, g);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) B.b[t] = q4k_bop(w, c, t);
+    B.bmin = c.bmin;
+    B.d = c.d;
+    B.dmin64 = c.dmin64;
     return B;
 }
 
@@ -332,11 +354,41 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
         for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);   // unconditional (clamped) prefetch
         __builtin_amdgcn_sched_barrier(0);
         if (active) {
-            ActOp A;
-            floatx4 rs;
-            load_act_units(A, rs, cur, lane);
+            // one K step at a time: the step's activation fragment is read
+            // once and each tile's B operand is built right before its MFMAs
+            WScale cs[R];
+            floatx4 am[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] += q4k_mma(q4k_wop(wc[r], g), A, g) * rs;
+            for (int r = 0; r < R; ++r) {
+                cs[r] = q4k_wscale(wc[r], g);
+                am[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const half8_t h = __builtin_bit_cast(half8_t, cur[(2 * t) * 64 + lane]);
+                const half8_t l = __builtin_bit_cast(half8_t, cur[(2 * t + 1) * 64 + lane]);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const half8_t bop = q4k_bop(wc[r], cs[r], t);
+                    am[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bop, am[r], 0, 0, 0);
+                    am[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bop, am[r], 0, 0, 0);
+                }
+            }
+            const half8_t ys = __builtin_bit_cast(half8_t, cur[1024 + lane]);
+            const float4 rv = __builtin_bit_cast(float4, cur[1088 + g]);
+            const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
+            const _Float16 z = (_Float16)0.f;
+            const bool on = g < 2;
+            const half4_t ysh = {on ? ys[0] : z, on ? ys[2] : z, on ? ys[4] : z, on ? ys[6] : z};
+            const half4_t ysl = {on ? ys[1] : z, on ? ys[3] : z, on ? ys[5] : z, on ? ys[7] : z};
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                floatx4 an = {0.f, 0.f, 0.f, 0.f};
+                an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, cs[r].bmin, an, 0, 0, 0);
+                an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, cs[r].bmin, an, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][i] += (cs[r].d * am[r][i] - cs[r].dmin64 * an[i]) * rs[i];
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
         SH_WAIT_VMCNT(0);                              // next block's units and weights have landed

@@ -16,13 +16,6 @@ int launch_add(float* y, const float* x, int64_t n, hipStream_t s);
 int launch_embed_rows(float* y, const float* W, const int32_t* tok, int T, int V, int D, hipStream_t s);
 int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int hd, const float* cs,
                      int max_pos, int* bad, hipStream_t s);
-// Per-row RMSNorm factor deferred to the consumer of a matmul: ssq holds
-// the sums of squares per 256-element block [rows][D/256] (nullptr = none).
-struct RowNorm {
-    const float* ssq;
-    int nblk, D;
-    float eps;
-};
 // Fused engine epilogues; `a` (nullable) receives the Q4_K activation operand
 // of rows_pad rows (rows past `rows` zero), y (nullable) the f32 rows.
 int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64_t split_stride, const float* w,

@@ -1,0 +1,46 @@
+// rowops.h -- device helpers of the row kernels: ordered split-K sums and
+// the deferred RMSNorm row factor.
+#pragma once
+#include "launch.h"
+
+namespace slate_hip {
+
+// sum_{k < n} p[k * stride] in split order (n >= 1), loads issued eight at a
+// time (clamped, so every address is a valid partial) and added under a
+// predicate, so the latency of the partials is paid once per eight splits.
+__device__ __forceinline__ float4 split_sum4(const float* p, int n, int64_t stride) {
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < n; k += 8) {
+        float4 t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = *(const float4*)(p + (int64_t)min(k + i, n - 1) * stride);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (k + i < n) { s.x += t[i].x; s.y += t[i].y; s.z += t[i].z; s.w += t[i].w; }
+    }
+    return s;
+}
+
+__device__ __forceinline__ float split_sum1(const float* p, int n, int64_t stride) {
+    float s = 0.f;
+    for (int k = 0; k < n; k += 8) {
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = p[(int64_t)min(k + i, n - 1) * stride];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (k + i < n) s += t[i];
+    }
+    return s;
+}
+
+// RMSNorm factor of row r from the per-256-block sums of squares that
+// residual_act_kernel leaves: inv = 1/sqrtf((float)(sum x^2 / D) + eps)
+// (backend_cpu.c:48-76; block sums added in double, in block order).
+__device__ __forceinline__ float row_inv_rms(const float* ssq, int r, int nblk, int D, float eps) {
+    double sq = 0.0;
+    for (int kb = 0; kb < nblk; ++kb) sq += (double)ssq[(size_t)r * nblk + kb];
+    return 1.0f / sqrtf((float)(sq / (double)D) + eps);
+}
+
+}  // namespace slate_hip

@@ -202,3 +202,36 @@ def test_deferred_rmsnorm_matches_row_rmsnorm(golden, monkeypatch):
         m.free()
     for a, b in zip(outs[0], outs[1]):
         assert relerr(a, b) < 1e-5
+
+
+FUSE = LlamaShape(n_layers=2, d_model=512, n_heads=8, n_kv_heads=4, ffn=768, vocab=300, max_seq=96)
+
+
+def test_q4k_decode_steps_match_oracle(orc):
+    """A 512-wide all-Q4_K model (every tensor 256-aligned, LM head Q4_K):
+    a prompt step for three sequences, then ragged decode steps, each
+    against the oracle (the CPU reference) replaying the same tokens."""
+    t = make_llama(FUSE, 4321, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, FUSE.vocab, n).astype(np.int32) for n in (6, 1, 11)]
+    m = slate_amd.Llama.from_tensors(FUSE, t, max_slots=4, max_tokens=32)
+    sess = [m.session() for _ in prompts]
+    rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+    assert rc == 0
+    steps = [lg]
+    toks = np.asarray(nxt, np.int32)
+    for _ in range(6):
+        rc, lg, nxt = m.step(sess, [1, 1, 1], toks)
+        assert rc == 0
+        steps.append(lg)
+        toks = np.asarray(nxt, np.int32)
+    om = OracleModel(orc, FUSE, t)
+    for i, p in enumerate(prompts):
+        o = om.session()
+        rc, want = o.prefill(p)
+        assert rc == 0 and relerr(steps[0][i], want) < TOL
+        tok = int(np.argmax(steps[0][i]))
+        for k in range(1, len(steps)):
+            rc, want = o.decode(tok)
+            assert rc == 0 and relerr(steps[k][i], want) < TOL, (i, k)
+            tok = int(np.argmax(steps[k][i]))
