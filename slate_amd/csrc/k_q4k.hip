@@ -7,6 +7,8 @@
 // nibble of byte i is element i, the high nibble element i+16.
 #include <string.h>
 
+#include <algorithm>
+
 #include "launch.h"
 #include "act16.h"
 
@@ -418,7 +420,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
 // through restrict pointers count as invariant and may be moved across the
 // barriers that order them here.
 template <int R, int NT, bool TILED, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(const uint8_t* W, int M, const uint4* frag, int act_tiles,
+__global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const uint4* frag, int act_tiles,
                                                      float* __restrict__ out, int64_t ldo,
                                                      int64_t split_stride, int nblk, int bps) {
     __shared__ uint4 s_act[2 * NT * ACT_FRAG_UNITS];
@@ -428,8 +430,15 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(const uint8_t* W, in
     const int j = lane & 15;
     const int g = lane >> 4;
     const int wv = tid >> 6;
+    // workgroup x -> tensor (tensors start on workgroup boundaries)
+    const int wg = blockIdx.x;
+    const int ti = (tg.n > 2 && wg >= tg.grp0[2]) ? 2 : ((tg.n > 1 && wg >= tg.grp0[1]) ? 1 : 0);
+    const uint8_t* W = ti == 2 ? tg.w[2] : (ti == 1 ? tg.w[1] : tg.w[0]);
+    const int M = ti == 2 ? tg.M[2] : (ti == 1 ? tg.M[1] : tg.M[0]);
+    const int col = ti == 2 ? tg.col[2] : (ti == 1 ? tg.col[1] : tg.col[0]);
+    const int wg0 = ti == 2 ? tg.grp0[2] : (ti == 1 ? tg.grp0[1] : tg.grp0[0]);
     const int tiles = (M + 15) / 16;
-    const int tile0 = (blockIdx.x * WAVES + wv) * R;
+    const int tile0 = ((wg - wg0) * WAVES + wv) * R;
     const bool active = tile0 < tiles;
     const int at0 = blockIdx.z * NT;
     const int kb0 = blockIdx.y * bps;
@@ -501,7 +510,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(const uint8_t* W, in
         for (int r = 0; r < R; ++r) wc[r] = wn[r];
     }
     if (!active) return;
-    float* o = out + (int64_t)blockIdx.y * split_stride;
+    float* o = out + (int64_t)blockIdx.y * split_stride + col;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int row = (tile0 + r) * 16 + j;
@@ -560,13 +569,25 @@ static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t
 constexpr int PF_R = 2, PF_WAVES = 8;
 
 template <int NT, bool TILED, int R = PF_R, int WAVES = PF_WAVES>
-static void launch_pf(const Q4kTarget& t, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk, int bps,
+static void launch_pf(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk, int bps,
                       int nsplit, hipStream_t s, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
-    const int tiles = (t.M + 15) / 16;
     const int act_tiles = a.rows_pad / 16;
-    dim3 grid((tiles + WAVES * R - 1) / (WAVES * R), nsplit, (act_tiles + NT - 1) / NT);
-    SH_LAUNCH(e0, e1, (q4k_pf_kernel<R, NT, TILED, WAVES>), grid, dim3(64 * WAVES), 0, s, (const uint8_t*)t.w, t.M,
-              (const uint4*)a.frag, act_tiles, out + t.col, ldo, ss, nblk, bps);
+    dim3 grid(tg.grp_end, nsplit, (act_tiles + NT - 1) / NT);
+    SH_LAUNCH(e0, e1, (q4k_pf_kernel<R, NT, TILED, WAVES>), grid, dim3(64 * WAVES), 0, s, tg, (const uint4*)a.frag,
+              act_tiles, out, ldo, ss, nblk, bps);
+}
+
+// Workgroup slots per CU of the prefill kernel (its LDS: NT tiles x 2 buffers).
+static int pf_slots(int NT) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    const int per_cu = (160 * 1024) / (2 * NT * ACT_FRAG_UNITS * 16);
+    return cus * (per_cu > 0 ? per_cu : 1);
 }
 
 int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo, int64_t split_stride,
@@ -578,25 +599,40 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
     if (max_splits < 1) max_splits = 1;
     const int act_tiles = a.rows_pad / 16;
     if (act_tiles > 1) {
-        // prefill: NT activation tiles per workgroup, splits only to fill the chip
-        static const int pf_target = env_int("SLATE_HIP_Q4K_PF_WGS", 256);
-        const int NT = act_tiles >= 4 ? 4 : (act_tiles >= 2 ? 2 : 1);
+        // prefill: all tensors in one launch, NT activation tiles per
+        // workgroup; the split count minimises the rounds of workgroups per
+        // unit of work (a last, partly filled round idles the chip)
+        const int NT = act_tiles >= 4 ? 4 : 2;
+        Q4kTargets tg{};
         int wgs = 0;
-        for (int i = 0; i < n; ++i)
-            wgs += ((t[i].M + 15) / 16 + PF_WAVES * PF_R - 1) / (PF_WAVES * PF_R) * ((act_tiles + NT - 1) / NT);
+        for (int i = 0; i < n; ++i) {
+            tg.w[i] = (const uint8_t*)t[i].w;
+            tg.M[i] = t[i].M;
+            tg.col[i] = (int)t[i].col;
+            tg.grp0[i] = wgs;
+            wgs += ((t[i].M + 15) / 16 + PF_WAVES * PF_R - 1) / (PF_WAVES * PF_R);
+        }
+        tg.n = n;
+        tg.grp_end = wgs;
+        const int tasks = wgs * ((act_tiles + NT - 1) / NT);
+        const int slots = pf_slots(NT);
         int S = 1;
-        while (S * 2 <= max_splits && S * 2 <= nblk / 2 && wgs * S < pf_target) S *= 2;
+        double best = 1e30;
+        for (int c = 1; c <= 8 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
+            const int rounds = (tasks * c + slots - 1) / slots;
+            const double cost = (double)rounds / c;
+            if (cost < best - 1e-9) { best = cost; S = c; }
+        }
+        static const int S_env = env_int("SLATE_HIP_Q4K_PF_S", 0);
+        if (S_env > 0) S = std::min(S_env, std::max(1, std::min(max_splits, nblk)));
         const int bps = (nblk + S - 1) / S;
         S = (nblk + bps - 1) / bps;
-        for (int i = 0; i < n; ++i) {
-            hipEvent_t e0 = i == 0 ? ev_start : nullptr, e1 = i == n - 1 ? ev_stop : nullptr;
-            if (NT == 4) {
-                if (tiled) launch_pf<4, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
-                else launch_pf<4, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
-            } else {
-                if (tiled) launch_pf<2, true>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
-                else launch_pf<2, false>(t[i], a, out, ldo, split_stride, nblk, bps, S, s, e0, e1);
-            }
+        if (NT == 4) {
+            if (tiled) launch_pf<4, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+            else launch_pf<4, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+        } else {
+            if (tiled) launch_pf<2, true>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+            else launch_pf<2, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
         }
         SH_CHECK_LAUNCH();
         *S_out = S;
