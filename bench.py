@@ -11,10 +11,11 @@ prefill + decode).  A step = one pass of the engine over the packed batch;
 each step produces one token per sequence.
 
 Printed: one JSON line.  value = generated tokens / wall time over K timed
-steps (weights and KV resident in HBM).  roofline = the dominant kernel class
-of the decode steps by device time (decode-shaped Q4_K matmuls or decode
-attention), from HIP events recorded on the backend stream around every
-launch in the timed steps: achieved = algorithmic bytes / device time;
+steps (weights and KV resident in HBM; decode-only steps replay captured HIP
+graphs).  roofline = the dominant kernel class of the decode steps by device
+time (decode-shaped Q4_K matmuls or decode attention), from HIP events that
+the kernel dispatches record themselves, in every 8th timed step (launched
+kernel by kernel for that purpose): achieved = algorithmic bytes / device time;
 traffic = HBM bytes per launch from the committed rocprofv3 PMC summary.
 cpu_baseline = slate's own C decode step (slate_llama_decode_step, single
 thread as wired) on the same weights and KV state, for one step of all 16
@@ -34,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s at B=16 ragged, 8B-shape Q4_K; Q4_K matmul HBM GB/s"
 HBM_PEAK_GBS = 8000.0
+PROFILE_EVERY = 8
 
 
 def log(*a):
@@ -153,24 +155,32 @@ def main():
         wl.step()
     lib = slate_amd.load_library()
     m.profile(True)
+    m.profile(False)
     lib.slate_hip_sync()
     arrivals0 = wl.arrivals
     mixed_steps = 0
-    step_s, step_mixed = [], []
+    step_s, step_mixed, step_prof = [], [], []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        # one step in PROFILE_EVERY is launched kernel by kernel with
+        # dispatch-recorded events (the roofline); the others replay graphs
+        prof = i % PROFILE_EVERY == 0
+        if prof:
+            m.profile(True, reset=False)
         ts = time.perf_counter()
         mixed = wl.step()[0]
         step_s.append(time.perf_counter() - ts)
+        if prof:
+            m.profile(False)
         step_mixed.append(mixed)
+        step_prof.append(prof)
         mixed_steps += mixed
     lib.slate_hip_sync()
     dt = time.perf_counter() - t0
     raw = m.profile_read()
-    m.profile(False)
     tokens = args.batch * args.steps
     value = tokens / dt
-    dec_s = [t for t, mx in zip(step_s, step_mixed) if not mx]
+    dec_s = [t for t, mx, p in zip(step_s, step_mixed, step_prof) if not mx and not p]
     mix_s = [t for t, mx in zip(step_s, step_mixed) if mx]
     log(f"{args.steps} steps in {dt:.3f} s, {mixed_steps} with arrivals ({wl.arrivals - arrivals0} arrivals); "
         f"decode-only step median {1e3 * np.median(dec_s) if dec_s else 0:.2f} ms, "

@@ -191,7 +191,9 @@ void  slate_hip_llama_free(slate_hip_llama_t* m);
 int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
                                    void* host_dst, int64_t cap, int* dtype);
 
-/* llama.h:124-139 semantics, device-resident. */
+/* llama.h:124-139 semantics, device-resident.  A session belongs to its
+ * engine: free every session before slate_hip_llama_free (as a slate
+ * session must not outlive its model). */
 slate_hip_llama_session_t* slate_hip_llama_session_new(slate_hip_llama_t* m);
 void  slate_hip_llama_session_free(slate_hip_llama_session_t* s);
 int   slate_hip_llama_session_position(const slate_hip_llama_session_t* s);
@@ -222,11 +224,19 @@ int   slate_hip_llama_session_kv(const slate_hip_llama_session_t* s, float* K, f
  * 1 = attention in decode-only steps, 2 = decode-only steps, 3 = Q4_K
  * matmuls over more rows, 4 = attention in steps carrying prompt chunks,
  * 5 = steps carrying prompt chunks.
- * profile(m, 1) resets the totals and starts recording, profile(m, 0) stops.
- * profile_read returns the summed device milliseconds, the summed
- * algorithmic bytes (weights once, K/V once per kv head and sequence,
+ * profile(m, 1) resets the totals and starts recording, profile(m, 2)
+ * resumes recording without a reset, profile(m, 0) stops.  Kernel classes
+ * are timed by events the dispatches record themselves (kernel start and
+ * end).  Steps run while recording are launched one kernel at a time, not
+ * from a graph.  profile_read returns the summed device milliseconds, the
+ * summed algorithmic bytes (weights once, K/V once per kv head and sequence,
  * activations in and out) and the launch count of a class. */
 int   slate_hip_llama_profile(slate_hip_llama_t* m, int enable);
+/* graphs(m, 1) (or SLATE_HIP_GRAPHS=1): decode-only steps (one token per
+ * session) are captured once per batch size into a HIP graph and replayed.
+ * Default off: every kernel is launched separately.  Same results either
+ * way.  No slate counterpart (slate has no device graphs). */
+int   slate_hip_llama_graphs(slate_hip_llama_t* m, int enable);
 int   slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes,
                                    int64_t* launches);
 

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -103,6 +104,7 @@ SIGNATURES = {
     "slate_hip_llama_batch_step": (C.c_int, [vp, vp, C.c_int, vp, vp]),
     "slate_hip_llama_session_kv": (C.c_int, [vp, vp, vp]),
     "slate_hip_llama_profile": (C.c_int, [vp, C.c_int]),
+    "slate_hip_llama_graphs": (C.c_int, [vp, C.c_int]),
     "slate_hip_llama_profile_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double),
                                                C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
 }
@@ -255,6 +257,8 @@ class Llama:
         self.h = handle
         self.cfg = cfg
         self.vocab = cfg.vocab
+        # sessions must be released before the engine that owns their slots
+        self._sessions = weakref.WeakSet()
 
     @staticmethod
     def config(shape):
@@ -298,6 +302,8 @@ class Llama:
 
     def free(self):
         if getattr(self, "h", None):
+            for s in list(self._sessions):
+                s.free()
             self.lib.slate_hip_llama_free(self.h)
             self.h = None
 
@@ -320,8 +326,15 @@ class Llama:
     def session(self):
         return Session(self)
 
-    def profile(self, enable=True):
-        check(self.lib.slate_hip_llama_profile(self.h, 1 if enable else 0), "profile")
+    def profile(self, enable=True, reset=True):
+        """Start (reset=True: from zero; False: keep the totals) or stop
+        recording kernel-class timings."""
+        mode = (1 if reset else 2) if enable else 0
+        check(self.lib.slate_hip_llama_profile(self.h, mode), "profile")
+
+    def graphs(self, enable=True):
+        """Replay decode-only steps from captured HIP graphs (default off)."""
+        check(self.lib.slate_hip_llama_graphs(self.h, 1 if enable else 0), "graphs")
 
     def profile_read(self):
         """{class: (device ms, algorithmic bytes, launches)}; *_pf classes are
@@ -351,10 +364,12 @@ class Session:
         self.h = m.lib.slate_hip_llama_session_new(m.h)
         if not self.h:
             raise HipError(f"session_new failed: {last_error()}")
+        m._sessions.add(self)
 
     def free(self):
         if getattr(self, "h", None):
-            self.m.lib.slate_hip_llama_session_free(self.h)
+            if self.m.h:   # the engine frees its live sessions first
+                self.m.lib.slate_hip_llama_session_free(self.h)
             self.h = None
 
     def __del__(self):

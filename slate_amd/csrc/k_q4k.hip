@@ -488,16 +488,53 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
         for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
         __builtin_amdgcn_sched_barrier(0);
         if (active) {
-            WOp B[R];
+            // one K step at a time: each tile's B operand is built once and
+            // used against every activation tile, so consecutive MFMAs
+            // belong to independent accumulators
+            WScale cs[R];
+            floatx4 am[R][NT];
 #pragma unroll
-            for (int r = 0; r < R; ++r) B[r] = q4k_wop(wc[r], g);
+            for (int r = 0; r < R; ++r) {
+                cs[r] = q4k_wscale(wc[r], g);
+#pragma unroll
+                for (int n = 0; n < NT; ++n) am[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                half8_t bop[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) bop[r] = q4k_bop(wc[r], cs[r], t);
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const uint4* sa = cur + n * ACT_FRAG_UNITS;
+                    const half8_t h = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
+                    const half8_t l = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bop[r], am[r][n], 0, 0, 0);
+                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bop[r], am[r][n], 0, 0, 0);
+                    }
+                }
+            }
+            const _Float16 z = (_Float16)0.f;
+            const bool on = g < 2;
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
-                ActOp A;
-                floatx4 rs;
-                load_act_units(A, rs, cur + n * ACT_FRAG_UNITS, lane);
+                const uint4* sa = cur + n * ACT_FRAG_UNITS;
+                const half8_t ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
+                const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
+                const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
+                const half4_t ysh = {on ? ys[0] : z, on ? ys[2] : z, on ? ys[4] : z, on ? ys[6] : z};
+                const half4_t ysl = {on ? ys[1] : z, on ? ys[3] : z, on ? ys[5] : z, on ? ys[7] : z};
 #pragma unroll
-                for (int r = 0; r < R; ++r) acc[r][n] += q4k_mma(B[r], A, g) * rs;
+                for (int r = 0; r < R; ++r) {
+                    floatx4 an = {0.f, 0.f, 0.f, 0.f};
+                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, cs[r].bmin, an, 0, 0, 0);
+                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, cs[r].bmin, an, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[r][n][i] += (cs[r].d * am[r][n][i] - cs[r].dmin64 * an[i]) * rs[i];
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);

@@ -79,3 +79,37 @@ def test_missing_library_fails_loudly(tmp_path):
             mod.load_library(str(tmp_path / "absent.so"))
     finally:
         mod._lib = saved
+
+
+class _RecordingLib:
+    """Stands in for the library to watch the wrapper's call order."""
+
+    def __init__(self):
+        self.calls = []
+        self.next = 100
+
+    def slate_hip_llama_session_new(self, h):
+        self.next += 1
+        self.calls.append(("new", self.next))
+        return self.next
+
+    def slate_hip_llama_session_free(self, h):
+        self.calls.append(("session_free", h))
+
+    def slate_hip_llama_free(self, h):
+        self.calls.append(("engine_free", h))
+
+
+def test_engine_free_releases_live_sessions_first():
+    """A session never reaches slate_hip_llama_session_free after its engine
+    is gone (the engine's slot list would be freed memory by then)."""
+    lib = _RecordingLib()
+    m = object.__new__(slate_amd.Llama)
+    m.lib, m.h, m._sessions = lib, 7, __import__("weakref").WeakSet()
+    a, b = slate_amd.Session(m), slate_amd.Session(m)
+    a.free()
+    m.free()
+    b.free()            # after the engine: no call
+    del a, b
+    assert lib.calls == [("new", 101), ("new", 102), ("session_free", 101), ("session_free", 102),
+                         ("engine_free", 7)]

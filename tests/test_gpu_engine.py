@@ -235,3 +235,48 @@ def test_q4k_decode_steps_match_oracle(orc):
             rc, want = o.decode(tok)
             assert rc == 0 and relerr(steps[k][i], want) < TOL, (i, k)
             tok = int(np.argmax(steps[k][i]))
+
+
+def test_graph_replayed_decode_steps_match_eager_launches(golden):
+    """Decode-only steps replay a captured HIP graph; interleaved with eager
+    prompt steps and repeated many times, every replay gives bit-identical
+    logits, next tokens and KV to the same steps launched kernel by kernel."""
+    t = make_llama(Q4, Q4_SEED, quant="q4k", output_quant="f32")
+    rng = np.random.default_rng(21)
+    prompts = [rng.integers(0, Q4.vocab, n).astype(np.int32) for n in (4, 9)]
+    late = rng.integers(0, Q4.vocab, 7).astype(np.int32)
+    runs = []
+    for use_graphs in (True, False):
+        m = slate_amd.Llama.from_tensors(Q4, t, max_slots=3, max_tokens=32)
+        m.graphs(use_graphs)
+        ss = [m.session() for _ in prompts]
+        out = []
+        rc, lg, nxt = m.step(ss, [len(p) for p in prompts], np.concatenate(prompts))
+        assert rc == 0
+        out.append((lg, nxt))
+        toks = np.asarray(nxt, np.int32)
+        for _ in range(5):                       # replays of the 2-session graph
+            rc, lg, nxt = m.step(ss, [1, 1], toks)
+            assert rc == 0
+            out.append((lg, nxt))
+            toks = np.asarray(nxt, np.int32)
+        s3 = m.session()                         # eager prompt step between replays
+        rc, lg, nxt = m.step(ss + [s3], [1, 1, len(late)], np.concatenate([toks, late]))
+        assert rc == 0
+        out.append((lg, nxt))
+        toks = np.asarray(nxt, np.int32)
+        for _ in range(5):                       # a second graph (3 sessions), replayed
+            rc, lg, nxt = m.step(ss + [s3], [1, 1, 1], toks)
+            assert rc == 0
+            out.append((lg, nxt))
+            toks = np.asarray(nxt, np.int32)
+        rc, lg, nxt = m.step(ss, [1, 1], toks[:2])   # back to the first graph
+        assert rc == 0
+        out.append((lg, nxt))
+        runs.append((out, [s.kv() for s in ss + [s3]]))
+        m.free()
+    (a, akv), (b, bkv) = runs
+    for (la, na), (lb, nb) in zip(a, b):
+        assert np.array_equal(la, lb) and np.array_equal(na, nb)
+    for (K1, V1), (K2, V2) in zip(akv, bkv):
+        assert np.array_equal(K1, K2) and np.array_equal(V1, V2)
