@@ -302,6 +302,194 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     }
 }
 
+// Sum and max over the 8 lanes of an aligned lane group, with DPP moves
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror): no LDS
+// crossbar traffic.  Every lane of the group gets the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float group8_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    return v;
+}
+__device__ __forceinline__ float group8_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    return v;
+}
+// Over the 8 lane groups of a wave (row_ror:8 pairs the two groups of a
+// 16-lane row; the rows exchange through two lane shuffles).
+__device__ __forceinline__ float wave_groups_max(float v) {
+    v = fmaxf(v, dpp_mov<0x128>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_groups_sum(float v) {
+    v += dpp_mov<0x128>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Decode work unit (one query token per sequence): (key chunk, token, kv
+// head), G query heads.  Each wave owns 64 keys of the 256-key chunk and
+// works through them without barriers:
+//   scores  8 lanes per key row (lane ls holds dims 32i + 4ls .. +3 of the
+//           row and of the G query slices; one load instruction of a wave
+//           covers 8 rows x 128 contiguous bytes), reduced over the 8 lanes
+//           by DPP; the wave's 8 x 8 scores per head stay in registers;
+//   softmax max and sum over the wave's keys;
+//   PV      the same lane owns the same key's V row slice, weighted by its
+//           own probability.
+// The waves then combine through LDS (log-sum-exp over the four wave
+// maxima) into the chunk partial (max m, sum l, unnormalised output), as
+// attn_block_kernel writes it.
+template <int HD, int G>
+__global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
+    const float* __restrict__ q, const float* __restrict__ Kp, const float* __restrict__ Vp,
+    const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
+    const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
+    float* __restrict__ pml) {
+    constexpr int NV = HD / 32;                    // float4 per lane per row
+    constexpr int KW = ATT_CHUNK / 4;              // keys per wave
+    constexpr int IT = KW / 8;                     // rounds of 8 keys
+    __shared__ float4 s_o[4][4][G][HD / 4];        // [wave][16-lane row][head][dims]
+    __shared__ float s_m[4][G], s_l[4][G];
+    const int c = blockIdx.x, h = blockIdx.z;
+    const int t = dec_t0 ? dec_t0[blockIdx.y] : blockIdx.y;
+    const int p = tok_pos[t];
+    const int k0 = c * ATT_CHUNK;
+    if (k0 > p) return;                            // merge never reads chunks past a token's end
+    const int nk = min(p + 1 - k0, ATT_CHUNK);
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int lg = lane >> 3, ls = lane & 7;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int64_t base = kv_base[tok2seq[t]] + (int64_t)h * head_stride + (int64_t)k0 * HD;
+    const float* Kh = Kp + base;
+    const float* Vh = Vp + base;
+    const int kw0 = wv * KW;
+    if (kw0 < nk) {
+        const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
+        float4 qv[G][NV];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) qv[gi][i] = *(const float4*)(qt + gi * HD + 32 * i + 4 * ls);
+        float sc[G][IT];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int j = kw0 + 8 * it + lg;
+            const float* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
+            float4 kv[NV];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) kv[i] = *(const float4*)(kr + 32 * i + 4 * ls);
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                float a = 0.f;
+#pragma unroll
+                for (int i = 0; i < NV; ++i) {
+                    a = __builtin_fmaf(qv[gi][i].x, kv[i].x, a);
+                    a = __builtin_fmaf(qv[gi][i].y, kv[i].y, a);
+                    a = __builtin_fmaf(qv[gi][i].z, kv[i].z, a);
+                    a = __builtin_fmaf(qv[gi][i].w, kv[i].w, a);
+                }
+                a = group8_sum(a);
+                sc[gi][it] = j < nk ? a * scale : -INFINITY;
+            }
+        }
+        float mx[G], sum[G];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            float m = sc[gi][0];
+#pragma unroll
+            for (int it = 1; it < IT; ++it) m = fmaxf(m, sc[gi][it]);
+            mx[gi] = wave_groups_max(m);           // finite: key kw0 is always inside the chunk
+            float l = 0.f;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const float e = sc[gi][it] == -INFINITY ? 0.f : expf(sc[gi][it] - mx[gi]);
+                sc[gi][it] = e;
+                l += e;
+            }
+            sum[gi] = wave_groups_sum(l);
+        }
+        float4 acc[G][NV];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) acc[gi][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int it = 0; it < IT; ++it) {
+            const int j = kw0 + 8 * it + lg;
+            const float* vr = Vh + (int64_t)min(j, nk - 1) * HD;
+            float4 vv[NV];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) vv[i] = *(const float4*)(vr + 32 * i + 4 * ls);
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                const float pj = sc[gi][it];
+#pragma unroll
+                for (int i = 0; i < NV; ++i) {
+                    acc[gi][i].x = __builtin_fmaf(pj, vv[i].x, acc[gi][i].x);
+                    acc[gi][i].y = __builtin_fmaf(pj, vv[i].y, acc[gi][i].y);
+                    acc[gi][i].z = __builtin_fmaf(pj, vv[i].z, acc[gi][i].z);
+                    acc[gi][i].w = __builtin_fmaf(pj, vv[i].w, acc[gi][i].w);
+                }
+            }
+        }
+        // the two lane groups of each 16-lane row; rows are summed below
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                acc[gi][i].x += dpp_mov<0x128>(acc[gi][i].x);
+                acc[gi][i].y += dpp_mov<0x128>(acc[gi][i].y);
+                acc[gi][i].z += dpp_mov<0x128>(acc[gi][i].z);
+                acc[gi][i].w += dpp_mov<0x128>(acc[gi][i].w);
+            }
+        if ((lane & 8) == 0)
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+                for (int i = 0; i < NV; ++i) s_o[wv][lane >> 4][gi][8 * i + ls] = acc[gi][i];
+        if (lane == 0)
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                s_m[wv][gi] = mx[gi];
+                s_l[wv][gi] = sum[gi];
+            }
+    }
+    __syncthreads();
+    const int nw = (nk + KW - 1) / KW;             // waves that had keys
+    for (int idx = tid; idx < G * (HD / 4); idx += ATT_THREADS) {
+        const int gi = idx / (HD / 4), d4 = idx - gi * (HD / 4);
+        float M = s_m[0][gi];
+        for (int w = 1; w < nw; ++w) M = fmaxf(M, s_m[w][gi]);
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.f;
+        for (int w = 0; w < nw; ++w) {
+            const float f = expf(s_m[w][gi] - M);
+            L += f * s_l[w][gi];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float4 v = s_o[w][r][gi][d4];
+                o.x += f * v.x; o.y += f * v.y; o.z += f * v.z; o.w += f * v.w;
+            }
+        }
+        const size_t pidx = ((size_t)t * Hq + h * G + gi) * nch_max + c;
+        *(float4*)(po + pidx * HD + 4 * d4) = o;
+        if (d4 == 0) {
+            pml[pidx * 2 + 0] = M;
+            pml[pidx * 2 + 1] = L;
+        }
+    }
+}
+
 // out[t, hq, :] = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c.  One wave per
 // 256 output elements of a token row (lane: 4 consecutive elements of one
 // head); with `act` the row also goes out as the Q4_K activation operand
@@ -382,17 +570,38 @@ size_t attention_partial_floats(int T, int Hq, int HD, int max_pos) {
     return (size_t)T * Hq * nch * (HD + 2);
 }
 
+// SLATE_HIP_ATTN_WAVE=0 selects the workgroup-phased decode kernel for every shape.
+static bool wave_kernel() {
+    static const bool on = getenv("SLATE_HIP_ATTN_WAVE") == nullptr || atoi(getenv("SLATE_HIP_ATTN_WAVE")) != 0;
+    return on;
+}
+
+// The wave kernel where its query slices and accumulators fit the registers
+// and the launch is a decode batch (a few query tokens, K/V streamed from
+// HBM); prompt tokens, whose K/V re-reads hit L2, run the phased kernel at
+// its higher occupancy.
+constexpr int ATT_WAVE_MAX_TOKENS = 64;
+
+template <int HD, int G>
+static void launch_dec_g(dim3 grid, hipStream_t s, const AttnArgs& a) {
+    if constexpr (G * HD <= 512) {
+        if (wave_kernel() && grid.y <= ATT_WAVE_MAX_TOKENS) {
+            SH_LAUNCH(a.ev0, nullptr, (attn_dec_wave_kernel<HD, G>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp,
+                      a.qt0, a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);
+            return;
+        }
+    }
+    SH_LAUNCH(a.ev0, nullptr, (attn_dec_kernel<HD, G>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,
+              a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);
+}
+
 template <int HD>
 static int launch_dec_hd(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
     switch (G) {
-#define SH_DEC(GG)                                                                                            \
-    case GG:                                                                                                  \
-        SH_LAUNCH(a.ev0, nullptr, (attn_dec_kernel<HD, GG>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp,  \
-                  a.qt0,                                                                                      \
-                           a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);    \
-        return 0;
-        SH_DEC(1) SH_DEC(2) SH_DEC(4) SH_DEC(8)
-#undef SH_DEC
+        case 1: launch_dec_g<HD, 1>(grid, s, a); return 0;
+        case 2: launch_dec_g<HD, 2>(grid, s, a); return 0;
+        case 4: launch_dec_g<HD, 4>(grid, s, a); return 0;
+        case 8: launch_dec_g<HD, 8>(grid, s, a); return 0;
         default: return -5;
     }
 }

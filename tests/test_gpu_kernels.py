@@ -324,11 +324,13 @@ def test_pack_batch_bitexact(orc):
 
 
 # ------------------------------------------------------------ attention
-@pytest.mark.parametrize("hd,Hq,Hkv", [(128, 32, 8), (16, 4, 2), (64, 8, 8)])
-def test_attention_ragged_vs_oracle(hip, orc, hd, Hq, Hkv):
+@pytest.mark.parametrize("hd,Hq,Hkv,extra", [(128, 32, 8, 0), (16, 4, 2, 0), (64, 8, 8, 0), (128, 64, 8, 0),
+                                              (64, 32, 4, 0), (32, 8, 4, 0), (128, 32, 8, 70), (64, 8, 8, 70)])
+def test_attention_ragged_vs_oracle(hip, orc, hd, Hq, Hkv, extra):
     """Per-token GQA attention over ragged per-sequence caches, one query per
     token (decode) and several consecutive queries of one sequence (prefill
-    chunk), lengths across chunk boundaries."""
+    chunk), lengths across chunk boundaries.  `extra` adds a 70-token prompt
+    chunk (launches of more than 64 query tokens take the phased kernel)."""
     lib = load_library()
     rng = np.random.default_rng(hd + Hq)
     max_seq = 4352
@@ -344,6 +346,8 @@ def test_attention_ragged_vs_oracle(hip, orc, hd, Hq, Hkv):
         tok_pos.append(L - 1)
     tok2seq += [5, 5, 5]               # a prefill chunk: positions 10..12 of sequence 5
     tok_pos += [10, 11, 12]
+    tok2seq += [6] * extra             # positions 300.. of sequence 6
+    tok_pos += list(range(300, 300 + extra))
     T = len(tok2seq)
     kv_base = (np.arange(nslot, dtype=np.int64)[::-1] * slot_stride).copy()   # slot b -> nslot-1-b
     q = rng.normal(0, 1, (T, Hq * hd)).astype(np.float32)
