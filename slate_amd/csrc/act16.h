@@ -14,6 +14,7 @@
 // times 2^-6 as hi + lo.
 #pragma once
 #include "common.h"
+#include "lanes.h"
 
 namespace slate_hip {
 
@@ -22,9 +23,7 @@ typedef _Float16 act_half4_t __attribute__((ext_vector_type(4)));
 // One wave writes block kb of row r; lane holds elements 4*lane .. 4*lane+3
 // (zeros for padding rows).  Every lane of the wave must call it.
 __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb, int lane, float4 v) {
-    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float mx = wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     int ex = 0;
     if (mx > 0.f && isfinite(mx)) {
         frexpf(mx, &ex);                          // mx = m * 2^ex, m in [0.5, 1)
@@ -41,9 +40,7 @@ __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb,
         l[i] = (_Float16)(vv[i] - (float)h[i]);
         sum += vv[i];
     }
-    sum += __shfl_xor(sum, 1, 64);                // 8 lanes = one 32-element sub-block
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
+    sum = group8_sum(sum);                        // 8 lanes = one 32-element sub-block
     const float ss = sum * (1.0f / 64.0f);
     const _Float16 sh = (_Float16)ss;
     const _Float16 sl = (_Float16)(ss - (float)sh);

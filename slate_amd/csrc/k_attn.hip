@@ -13,6 +13,7 @@
 // combines the chunks with log-sum-exp rescaling.
 #include "launch.h"
 #include "act16.h"
+#include "lanes.h"
 
 namespace slate_hip {
 
@@ -104,8 +105,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_block_kernel(
             if (r < R) {
                 float v0 = sp[r * ATT_THREADS + lane], v1 = sp[r * ATT_THREADS + lane + 64];
                 float v2 = sp[r * ATT_THREADS + lane + 128], v3 = sp[r * ATT_THREADS + lane + 192];
-                float mx = fmaxf(fmaxf(v0, v1), fmaxf(v2, v3));
-                for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                const float mx = wave_max(fmaxf(fmaxf(v0, v1), fmaxf(v2, v3)));
                 const float mnew = fmaxf(m_run[j], mx);
                 const float alpha = m_run[j] == -INFINITY ? 0.f : expf(m_run[j] - mnew);
                 float e0 = v0 == -INFINITY ? 0.f : expf(v0 - mnew);
@@ -116,8 +116,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_block_kernel(
                 sp[r * ATT_THREADS + lane + 64] = e1;
                 sp[r * ATT_THREADS + lane + 128] = e2;
                 sp[r * ATT_THREADS + lane + 192] = e3;
-                float s = (e0 + e1) + (e2 + e3);
-                for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+                const float s = wave_sum((e0 + e1) + (e2 + e3));
                 l_run[j] = l_run[j] * alpha + s;
                 m_run[j] = mnew;
                 if (lane == 0) salpha[r] = alpha;
@@ -233,9 +232,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
                 a = __builtin_fmaf(qv[gi][i].z, kv[i].z, a);
                 a = __builtin_fmaf(qv[gi][i].w, kv[i].w, a);
             }
-            a += __shfl_xor(a, 1, 64);
-            a += __shfl_xor(a, 2, 64);
-            a += __shfl_xor(a, 4, 64);
+            a = group8_sum(a);
             if (ls == 0) sp[gi][j] = j < nk ? a * scale : -INFINITY;
         }
     }
@@ -244,7 +241,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     for (int gi = wv; gi < G; gi += 4) {
         float mx = -INFINITY;
         for (int j = lane; j < nkp; j += 64) mx = fmaxf(mx, sp[gi][j]);
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        mx = wave_max(mx);
         float sum = 0.f;
         for (int j = lane; j < nkp; j += 64) {
             const float sc = sp[gi][j];
@@ -252,7 +249,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
             sp[gi][j] = e;
             sum += e;
         }
-        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        sum = wave_sum(sum);
         if (lane == 0) {
             const size_t pidx = ((size_t)t * Hq + h * G + gi) * nch_max + c;
             pml[pidx * 2 + 0] = mx;
@@ -300,40 +297,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
         const size_t pidx = ((size_t)t * Hq + h * G + gi) * nch_max + c;
         *(float4*)(po + pidx * HD + 4 * dd) = o;
     }
-}
-
-// Sum and max over the 8 lanes of an aligned lane group, with DPP moves
-// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror): no LDS
-// crossbar traffic.  Every lane of the group gets the result.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float group8_sum(float v) {
-    v += dpp_mov<0xB1>(v);
-    v += dpp_mov<0x4E>(v);
-    v += dpp_mov<0x141>(v);
-    return v;
-}
-__device__ __forceinline__ float group8_max(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    return v;
-}
-// Over the 8 lane groups of a wave (row_ror:8 pairs the two groups of a
-// 16-lane row; the rows exchange through two lane shuffles).
-__device__ __forceinline__ float wave_groups_max(float v) {
-    v = fmaxf(v, dpp_mov<0x128>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
-}
-__device__ __forceinline__ float wave_groups_sum(float v) {
-    v += dpp_mov<0x128>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
 }
 
 // Decode work unit (one query token per sequence): (key chunk, token, kv
@@ -447,10 +410,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                acc[gi][i].x += dpp_mov<0x128>(acc[gi][i].x);
-                acc[gi][i].y += dpp_mov<0x128>(acc[gi][i].y);
-                acc[gi][i].z += dpp_mov<0x128>(acc[gi][i].z);
-                acc[gi][i].w += dpp_mov<0x128>(acc[gi][i].w);
+                acc[gi][i].x += dpp_mov<DPP_ROW_ROR8>(acc[gi][i].x);
+                acc[gi][i].y += dpp_mov<DPP_ROW_ROR8>(acc[gi][i].y);
+                acc[gi][i].z += dpp_mov<DPP_ROW_ROR8>(acc[gi][i].z);
+                acc[gi][i].w += dpp_mov<DPP_ROW_ROR8>(acc[gi][i].w);
             }
         if ((lane & 8) == 0)
 #pragma unroll

@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x
         sq = __builtin_fmaf(xv.y, xv.y, sq);
         sq = __builtin_fmaf(xv.z, xv.z, sq);
         sq = __builtin_fmaf(xv.w, xv.w, sq);
-        for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o, 64);
+        sq = wave_sum(sq);
         if (lane == 0) ssq[(size_t)r * nblk + kb] = sq;
         const float4 wv = *(const float4*)(w + e);
         yv = make_float4(xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w);
