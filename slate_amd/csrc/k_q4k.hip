@@ -335,7 +335,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
             lds_copy16(frag + (size_t)kb * ACT_FRAG_UNITS + c * 64 + lane,
                        __builtin_amdgcn_readfirstlane(lds_addr(dst + c * 64)));
     };
-    WTile wc[R], wn[R];
+    WTile w0[R], w1[R];
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -343,11 +343,13 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
     stage(s_act, kb0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
+    for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
     __builtin_amdgcn_sched_barrier(0);
     SH_WAIT_VMCNT(0);
     __syncthreads();
-    for (int b = 0; b < nb; ++b) {
+    // block b from wc (landed) while wn receives block b+1; the two register
+    // sets swap roles each step (the loop is unrolled by two)
+    auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
         const uint4* cur = s_act + (b & 1) * ACT_FRAG_UNITS;
         const int kn = kb0 + min(b + 1, nb - 1);
         if (b + 1 < nb) stage(s_act + ((b + 1) & 1) * ACT_FRAG_UNITS, kn);
@@ -395,9 +397,13 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
         __builtin_amdgcn_sched_barrier(0);
         SH_WAIT_VMCNT(0);                              // next block's units and weights have landed
         __syncthreads();
-#pragma unroll
-        for (int r = 0; r < R; ++r) wc[r] = wn[r];
+    };
+    int b = 0;
+    for (; b + 2 <= nb; b += 2) {
+        step(w0, w1, b);
+        step(w1, w0, b + 1);
     }
+    if (b < nb) step(w0, w1, b);
     if (!active) return;
     float* o = out + (int64_t)blockIdx.y * split_stride + col;
 #pragma unroll
@@ -464,7 +470,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
             lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + n * ACT_FRAG_UNITS + u)));
         }
     };
-    WTile wc[R], wn[R];
+    WTile w0[R], w1[R];
     floatx4 acc[R][NT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -474,11 +480,12 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     stage(s_act, kb0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
+    for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
     __builtin_amdgcn_sched_barrier(0);
     SH_WAIT_VMCNT(0);
     __syncthreads();
-    for (int b = 0; b < nb; ++b) {
+    // the two weight register sets swap roles each step (unrolled by two)
+    auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
         // compute block b from one buffer while the other receives block b+1
         const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
         const int kn = kb0 + min(b + 1, nb - 1);
@@ -543,9 +550,13 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
         // load counting from also waiting on the next step's LDS copies
         SH_WAIT_VMCNT(0);
         __syncthreads();
-#pragma unroll
-        for (int r = 0; r < R; ++r) wc[r] = wn[r];
+    };
+    int b = 0;
+    for (; b + 2 <= nb; b += 2) {
+        step(w0, w1, b);
+        step(w1, w0, b + 1);
     }
+    if (b < nb) step(w0, w1, b);
     if (!active) return;
     float* o = out + (int64_t)blockIdx.y * split_stride + col;
 #pragma unroll
