@@ -365,6 +365,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
                 sc[gi][it] = j < nk ? a * scale : -INFINITY;
             }
         }
+        // the first V rows go out before the softmax (which needs no memory),
+        // into the registers the K rows no longer use
+        constexpr int VP = IT / 4;
+        float4 vpre[VP][NV];
+#pragma unroll
+        for (int it = 0; it < VP; ++it) {
+            const float* vr = Vh + (int64_t)min(kw0 + 8 * it + lg, nk - 1) * HD;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) vpre[it][i] = *(const float4*)(vr + 32 * i + 4 * ls);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         float mx[G], sum[G];
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
@@ -392,7 +403,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
             const float* vr = Vh + (int64_t)min(j, nk - 1) * HD;
             float4 vv[NV];
 #pragma unroll
-            for (int i = 0; i < NV; ++i) vv[i] = *(const float4*)(vr + 32 * i + 4 * ls);
+            for (int i = 0; i < NV; ++i) vv[i] = it < VP ? vpre[it][i] : *(const float4*)(vr + 32 * i + 4 * ls);
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 const float pj = sc[gi][it];
