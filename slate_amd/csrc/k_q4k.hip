@@ -282,7 +282,7 @@ __device__ __forceinline__ void load_act_units(ActOp& A, floatx4& rs, const uint
 // LDS-DMA tracking would stall the weight prefetch too); callers wait with
 // SH_WAIT_VMCNT and a barrier before reading the copied units.
 __device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(lds) : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
             lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + n * ACT_FRAG_UNITS + u)));
         }
     };
-    WTile w0[R], w1[R];
+    WTile wc[R], wn[R];
     floatx4 acc[R][NT];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -480,12 +480,13 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     stage(s_act, kb0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
+    for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
     __builtin_amdgcn_sched_barrier(0);
     SH_WAIT_VMCNT(0);
     __syncthreads();
-    // the two weight register sets swap roles each step (unrolled by two)
-    auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
+    // (swapping two register sets instead of copying, as the decode kernel
+    // does, costs this kernel 30 more VGPRs and 8 % at T = 320)
+    for (int b = 0; b < nb; ++b) {
         // compute block b from one buffer while the other receives block b+1
         const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
         const int kn = kb0 + min(b + 1, nb - 1);
@@ -550,13 +551,9 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
         // load counting from also waiting on the next step's LDS copies
         SH_WAIT_VMCNT(0);
         __syncthreads();
-    };
-    int b = 0;
-    for (; b + 2 <= nb; b += 2) {
-        step(w0, w1, b);
-        step(w1, w0, b + 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) wc[r] = wn[r];
     }
-    if (b < nb) step(w0, w1, b);
     if (!active) return;
     float* o = out + (int64_t)blockIdx.y * split_stride + col;
 #pragma unroll
