@@ -171,28 +171,24 @@ __device__ __forceinline__ float f16_to_f32_hw(uint32_t h) {
 
 // Per-block constants of one weight tile for lane group g: the f16 fma
 // terms that turn nibbles into q * sc (low nibble: 1024+q -> (1024+q)*sc -
-// 1024*sc; high nibble: 1024+16q -> ((1024+16q)*sc - 1024*sc)/16), the
-// sub-block mins as the min-term operand, d and 64 * dmin.
-struct WScale { half2_t lm0, lm1, la0, la1, hm0, hm1, ha0, ha1; half4_t bmin; float d, dmin64; };
+// 1024*sc; high nibble: 1024+16q -> (1024+16q)*(sc/16) - 64*sc), the
+// sub-block mins as the min-term operand, d and 64 * dmin.  Each half2 holds
+// sub-block 2g in .x and 2g+1 in .y; the B-operand fma broadcasts one half.
+struct WScale { half2_t sc, lo_add, hi_mul, hi_add; half4_t bmin; float d, dmin64; };
 
 __device__ __forceinline__ WScale q4k_wscale(const WTile& w, int g) {
     WScale c;
     ScaleBytes sb = unpack_scales(w.hdr.y, w.hdr.z, w.hdr.w);
-    uint32_t scw = g < 2 ? sb.sc_lo : sb.sc_hi;
-    int sh = 16 * (g & 1);
-    _Float16 s0 = (_Float16)(float)((scw >> sh) & 0xffu);
-    _Float16 s1 = (_Float16)(float)((scw >> (sh + 8)) & 0xffu);
-    c.lm0 = half2_t{s0, s0};
-    c.lm1 = half2_t{s1, s1};
-    c.la0 = c.lm0 * (_Float16)-1024.0f;
-    c.la1 = c.lm1 * (_Float16)-1024.0f;
-    c.hm0 = c.lm0 * (_Float16)0.0625f;
-    c.hm1 = c.lm1 * (_Float16)0.0625f;
-    c.ha0 = c.lm0 * (_Float16)-64.0f;
-    c.ha1 = c.lm1 * (_Float16)-64.0f;
+    const uint32_t scw = g < 2 ? sb.sc_lo : sb.sc_hi;
+    // bytes 2(g&1), 2(g&1)+1 as 1024 + sc in f16, minus 1024 (exact)
+    const uint32_t sel = (g & 1) ? 0x04030402u : 0x04010400u;
+    const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    c.sc = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, scw, sel)) + k1024;
+    c.lo_add = c.sc * (_Float16)-1024.0f;
+    c.hi_mul = c.sc * (_Float16)0.0625f;
+    c.hi_add = c.sc * (_Float16)-64.0f;
     // mins of sub-blocks 4g..4g+3 for g < 2 (groups 2, 3 carry the zero padding
     // on the activation side, so their values do not matter)
-    const half2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
     const uint32_t mw = (g & 1) ? sb.mn_hi : sb.mn_lo;
     const half2_t m01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) + k1024;
     const half2_t m23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) + k1024;
@@ -210,8 +206,10 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
     const uint32_t mask = (tq & 2) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
     const uint32_t w0 = ((tq & 1) ? Q.z : Q.x) & mask;
     const uint32_t w1 = ((tq & 1) ? Q.w : Q.y) & mask;
-    const half2_t mul = (tq & 2) ? (t < 4 ? c.hm0 : c.hm1) : (t < 4 ? c.lm0 : c.lm1);
-    const half2_t add = (tq & 2) ? (t < 4 ? c.ha0 : c.ha1) : (t < 4 ? c.la0 : c.la1);
+    const half2_t mv = (tq & 2) ? c.hi_mul : c.sc;
+    const half2_t av = (tq & 2) ? c.hi_add : c.lo_add;
+    const _Float16 m = t < 4 ? mv.x : mv.y, a = t < 4 ? av.x : av.y;
+    const half2_t mul = {m, m}, add = {a, a};
     half2_t p0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u));
     half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u));
     half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u));
