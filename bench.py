@@ -11,16 +11,25 @@ prefill + decode).  A step = one pass of the engine over the packed batch;
 each step produces one token per sequence.
 
 Printed: one JSON line.  value = generated tokens / wall time over K timed
-steps (weights and KV resident in HBM; decode-only steps replay captured HIP
-graphs).  roofline = the dominant kernel class of the decode steps by device
-time (decode-shaped Q4_K matmuls or decode attention), from HIP events that
-the kernel dispatches record themselves, in every 8th timed step (launched
-kernel by kernel for that purpose): achieved = algorithmic bytes / device time;
-traffic = HBM bytes per launch from the committed rocprofv3 PMC summary.
-cpu_baseline = slate's own C decode step (slate_llama_decode_step, single
-thread as wired) on the same weights and KV state, for one step of all 16
-sequences.  --copy-calibration instead runs a plain device copy of known
-size (for scaling the PMC byte counters).
+steps (weights and KV resident in HBM).  roofline = the dominant kernel class
+of the decode steps by device time (decode-shaped Q4_K matmuls or decode
+attention), from HIP events that the kernel dispatches record themselves, in
+every 8th timed step: achieved = algorithmic bytes / device time; traffic =
+HBM bytes per launch from the committed rocprofv3 PMC summary.  cpu_baseline =
+slate's own C decode step (slate_llama_decode_step, single thread as wired)
+on the same weights and KV state, for one step of all 16 sequences.
+kernels.hbm_copy_GBs = a measured 1 GiB device copy (read + write bytes /
+time) beside the nominal 8 TB/s.
+
+--ops instead prints the op-level figures (one JSON object): the Q4_K matmul
+through the C ABI at (M, K) in {(4096, 4096), (14336, 4096), (4096, 14336)}
+and B in {1, 4, 16, 64}, rotating over enough weight copies (> 300 MB) that
+the 256 MB Infinity Cache cannot hold them; and ragged GQA attention with
+B = 64 sequences, 32 q / 8 kv heads, head_dim 128, lengths
+clip(round(exp(N(ln 1024, 1))), 16, 16384).  Each figure is the device time
+of a captured graph of many calls (no host launch gaps) divided by the calls.
+--copy-calibration instead runs a plain device copy of known size (for
+scaling the PMC byte counters).
 """
 import argparse
 import json
@@ -121,6 +130,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device-to-device copy 5 times and exit")
+    ap.add_argument("--ops", action="store_true", help="op-level Q4_K matmul and ragged attention figures")
     args = ap.parse_args()
     if args.copy_calibration:
         import torch
@@ -136,6 +146,13 @@ def main():
         print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU sharding is described "
                                    "in DESIGN.md and not executed", "n_gpus": args.gpus}))
         return 2
+    if args.ops:
+        print(json.dumps(run_ops(args.seed)), flush=True)
+        return 0
+    try:   # torch (for the copy-bandwidth figure) must initialise HIP before the library does
+        import torch  # noqa: F401
+    except ImportError:
+        pass
 
     import slate_amd
     from slate_amd.synth import LlamaShape
@@ -220,6 +237,11 @@ def main():
                     "mixed_step_ms": [round(1e3 * t, 1) for t in mix_s],
                     "prefill_q4k_ms": round(pf_ms, 2), "prefill_q4k_launches": pf_n},
     }
+    try:
+        result["kernels"]["hbm_copy_GBs"] = round(copy_bandwidth(), 1)
+    except Exception as e:  # reported beside the nominal peak, never required
+        result["kernels"]["hbm_copy_GBs"] = None
+        log(f"copy bandwidth not measured: {e}")
     if not args.no_cpu:
         try:
             result["cpu_baseline"] = cpu_baseline_and_parity(m, shape, wl)
@@ -227,6 +249,126 @@ def main():
             result["cpu_baseline"] = {"error": str(e)}
     print(json.dumps(result), flush=True)
     return 0
+
+
+def copy_bandwidth(reps=10):
+    """Device copy of 1 GiB (read + written bytes / device time), GB/s."""
+    import torch
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del a, b
+    return 2 * 4 * n / (ms * 1e-3) / 1e9
+
+
+def graph_time_us(fn, calls, stream, result):
+    """Device microseconds per call of fn (which enqueues on the backend
+    stream), from a graph of `calls` captured calls replayed three times, and
+    whether every replay left `result` (the output tensor, the same for every
+    call) equal to the eager call's."""
+    import torch
+    fn(0)                                        # eager; grows scratch outside the capture
+    torch.cuda.synchronize()
+    ref = result.clone()
+    same = True
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(calls):
+            fn(i)
+    best = None
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record()
+            g.replay()
+            e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / calls
+        best = us if best is None else min(best, us)
+        same = same and bool(torch.equal(result, ref))
+        result.zero_()
+        torch.cuda.synchronize()
+    del g
+    return best, same
+
+
+def run_ops(seed):
+    """C2 (Q4_K matmul) and C3 (ragged attention) op figures."""
+    import torch
+    import slate_amd
+    lib = slate_amd.load_library()
+    slate_amd.Backend()
+    stream = torch.cuda.ExternalStream(lib.slate_hip_stream())
+    out = {"metric": "op-level device time per call", "hbm_peak_GBs": HBM_PEAK_GBS,
+           "mfma_f16_peak_TFLOPs": 2500.0, "hbm_copy_GBs": round(copy_bandwidth(), 1), "q4k": [],
+           "attention": None}
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for M, K in ((4096, 4096), (14336, 4096), (4096, 14336)):
+        nblk = M * K // 256
+        raw = torch.randint(0, 256, (nblk, 144), dtype=torch.uint8, device="cuda", generator=gen)
+        raw[:, 1] = (raw[:, 1] & 0x1F) | 0x10        # finite, moderate d and dmin
+        raw[:, 3] = (raw[:, 3] & 0x1F) | 0x10
+        tb = lib.slate_hip_q4k_tiled_bytes(M, K)
+        ncopy = max(32, -(-300_000_000 // tb) + 1)
+        copies = torch.empty((ncopy, tb), dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        for c in range(ncopy):
+            slate_amd.check(lib.slate_hip_q4k_tile(copies[c].data_ptr(), raw.data_ptr(), M, K), "q4k_tile")
+        lib.slate_hip_sync()
+        del raw
+        for B in (1, 4, 16, 64):
+            X = torch.randn(B, K, device="cuda", generator=gen)
+            Y = torch.empty(B, M, device="cuda")
+            torch.cuda.synchronize()
+
+            def call(i, X=X, Y=Y, B=B):
+                slate_amd.check(lib.slate_hip_matmul_q4k_tiled(Y.data_ptr(), copies[i % ncopy].data_ptr(),
+                                                               X.data_ptr(), B, M, K), "matmul_q4k_tiled")
+            us, same = graph_time_us(call, 2 * ncopy, stream, Y)
+            alg = M * K // 256 * 144 + 4 * B * K + 4 * B * M
+            flops = 2.0 * B * M * K
+            out["q4k"].append({"M": M, "K": K, "B": B, "us": round(us, 2),
+                               "GBs": round(alg / us / 1e3, 1), "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 3),
+                               "TFLOPs": round(flops / us / 1e6, 1),
+                               "frac_mfma": round(flops / us / 1e6 / 2500.0, 4), "replays_match_eager": same})
+            log(out["q4k"][-1])
+        del copies
+        torch.cuda.empty_cache()
+    # C3: ragged attention
+    rng = np.random.default_rng(seed)
+    Bq, Hq, Hkv, hd = 64, 32, 8, 128
+    L = np.clip(np.round(np.exp(rng.normal(np.log(1024.0), 1.0, Bq))), 16, 16384).astype(np.int64)
+    max_seq = int(L.max())
+    head_stride = max_seq * hd
+    slot = Hkv * head_stride
+    Kp = torch.randn(Bq * slot, device="cuda", generator=gen)
+    Vp = torch.randn(Bq * slot, device="cuda", generator=gen)
+    q = torch.randn(Bq, Hq * hd, device="cuda", generator=gen)
+    o = torch.empty_like(q)
+    t2s = torch.arange(Bq, dtype=torch.int32, device="cuda")
+    pos = torch.tensor(L - 1, dtype=torch.int32, device="cuda")
+    kvb = torch.arange(Bq, dtype=torch.int64, device="cuda") * slot
+    torch.cuda.synchronize()
+
+    def att(i):
+        slate_amd.check(lib.slate_hip_attention_ragged(o.data_ptr(), q.data_ptr(), Kp.data_ptr(), Vp.data_ptr(),
+                                                       t2s.data_ptr(), pos.data_ptr(), kvb.data_ptr(), Bq, Hq,
+                                                       Hkv, hd, head_stride, max_seq), "attention_ragged")
+    us, same = graph_time_us(att, 20, stream, o)
+    alg = int(L.sum()) * 2 * Hkv * hd * 4 + 2 * Bq * Hq * hd * 4
+    out["attention"] = {"B": Bq, "Hq": Hq, "Hkv": Hkv, "head_dim": hd, "sum_L": int(L.sum()),
+                        "max_L": max_seq, "us": round(us, 2), "GBs": round(alg / us / 1e3, 1),
+                        "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 3), "replays_match_eager": same}
+    log(out["attention"])
+    return out
 
 
 def measured_traffic(kernel):

@@ -433,6 +433,8 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                                m->last_tok, m->status, s);
     if (rc) return rc;
     if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
+    // the decode attention work units depend only on positions: once per step
+    if ((rc = launch_attention_pairs(d_blk, m->n_dec, m->tok_pos, T, c.n_heads, c.max_seq, m->att_pml, s))) return rc;
     const int tpad = row_pad(T);
     int S_prev = 0;
     RowNorm rn{};
@@ -473,7 +475,8 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
                                               m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
                                               c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
-                                              m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea), prof_ev(m, eb))))
+                                              m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea), prof_ev(m, eb),
+                                              true)))
                 return rc;
             if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
                 m->prof_recs.push_back({m->step_mixed ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, eb});

@@ -172,6 +172,44 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_block_kernel(
     }
 }
 
+// The (decode token, key chunk) work units that hold keys, in token order:
+// pairs[0] = count, pairs[1 + u] = i * 65536 + c for token list entry i
+// (dec_t0[i], or i) and chunk c < ceil((pos + 1) / ATT_CHUNK).  One
+// workgroup; a block-wide scan per 1024 tokens.  Decode kernels launch
+// n_dec * nch_max units along x and take unit u from this list, so every
+// unit that streams keys is dispatched before the empty ones.
+__global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restrict__ dec_t0, int n_dec,
+                                                          const int32_t* __restrict__ tok_pos, int nch_max,
+                                                          int32_t* __restrict__ pairs) {
+    __shared__ int s_scan[1024];
+    __shared__ int s_base;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_base = 0;
+    __syncthreads();
+    for (int i0 = 0; i0 < n_dec; i0 += 1024) {
+        const int i = i0 + tid;
+        int n = 0;
+        if (i < n_dec) {
+            const int t = dec_t0 ? dec_t0[i] : i;
+            n = min((tok_pos[t] + ATT_CHUNK) / ATT_CHUNK, nch_max);
+        }
+        s_scan[tid] = n;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            const int v = tid >= o ? s_scan[tid - o] : 0;
+            __syncthreads();
+            s_scan[tid] += v;
+            __syncthreads();
+        }
+        const int base = s_base + s_scan[tid] - n;
+        for (int c = 0; c < n; ++c) pairs[1 + base + c] = i * 65536 + c;
+        __syncthreads();
+        if (tid == 1023) s_base += s_scan[1023];
+        __syncthreads();
+    }
+    if (tid == 0) pairs[0] = s_base;
+}
+
 // Decode work unit (one query token per sequence): (key chunk, token, kv
 // head), G query heads.  Every K and V row of the chunk is read once, whole
 // and coalesced:
@@ -188,14 +226,18 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     const float* __restrict__ q, const float* __restrict__ Kp, const float* __restrict__ Vp,
     const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
     const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
-    float* __restrict__ pml) {
+    float* __restrict__ pml, const int32_t* __restrict__ pairs) {
     constexpr int NV = HD / 32;
     constexpr int LPR = HD / 4;
     constexpr int KPI = 64 / LPR;
     __shared__ float sp[G][ATT_CHUNK];
     __shared__ float4 sred[4][G][LPR];
-    const int c = blockIdx.x, h = blockIdx.z;
-    const int t = dec_t0 ? dec_t0[blockIdx.y] : blockIdx.y;
+    // work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
+    // wrote; the units past its count are the grid's empty tail
+    if ((int)blockIdx.x >= pairs[0]) return;
+    const int pr = pairs[1 + blockIdx.x];
+    const int c = pr & 0xffff, h = blockIdx.z;
+    const int t = dec_t0 ? dec_t0[pr >> 16] : (pr >> 16);
     const int p = tok_pos[t];
     const int k0 = c * ATT_CHUNK;
     if (k0 > p) return;                            // merge never reads chunks past a token's end
@@ -317,14 +359,18 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
     const float* __restrict__ q, const float* __restrict__ Kp, const float* __restrict__ Vp,
     const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
     const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
-    float* __restrict__ pml) {
+    float* __restrict__ pml, const int32_t* __restrict__ pairs) {
     constexpr int NV = HD / 32;                    // float4 per lane per row
     constexpr int KW = ATT_CHUNK / 4;              // keys per wave
     constexpr int IT = KW / 8;                     // rounds of 8 keys
     __shared__ float4 s_o[4][4][G][HD / 4];        // [wave][16-lane row][head][dims]
     __shared__ float s_m[4][G], s_l[4][G];
-    const int c = blockIdx.x, h = blockIdx.z;
-    const int t = dec_t0 ? dec_t0[blockIdx.y] : blockIdx.y;
+    // work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
+    // wrote; the units past its count are the grid's empty tail
+    if ((int)blockIdx.x >= pairs[0]) return;
+    const int pr = pairs[1 + blockIdx.x];
+    const int c = pr & 0xffff, h = blockIdx.z;
+    const int t = dec_t0 ? dec_t0[pr >> 16] : (pr >> 16);
     const int p = tok_pos[t];
     const int k0 = c * ATT_CHUNK;
     if (k0 > p) return;                            // merge never reads chunks past a token's end
@@ -484,15 +530,36 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
         const int L = tok_pos[t] + 1;
         const int nch = min((L + ATT_CHUNK - 1) / ATT_CHUNK, nch_max);
         const size_t p0 = ((size_t)t * Hq + hq) * nch_max;
+        // partials are loaded eight chunks at a time (clamped to the last
+        // chunk, used under a predicate) and combined in chunk order
+        constexpr int MB = 8;
         float M = -INFINITY;
-        for (int c = 0; c < nch; ++c) M = fmaxf(M, pml[(p0 + c) * 2]);
+        for (int c0 = 0; c0 < nch; c0 += MB) {
+            float mv[MB];
+#pragma unroll
+            for (int i = 0; i < MB; ++i) mv[i] = pml[(p0 + min(c0 + i, nch - 1)) * 2];
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                if (c0 + i < nch) M = fmaxf(M, mv[i]);
+        }
         float den = 0.f;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int c = 0; c < nch; ++c) {
-            const float f = expf(pml[(p0 + c) * 2] - M);
-            den += f * pml[(p0 + c) * 2 + 1];
-            const float4 o = *(const float4*)(po + (p0 + c) * HD + d);
-            acc.x += f * o.x; acc.y += f * o.y; acc.z += f * o.z; acc.w += f * o.w;
+        for (int c0 = 0; c0 < nch; c0 += MB) {
+            float2 ml[MB];
+            float4 ov[MB];
+#pragma unroll
+            for (int i = 0; i < MB; ++i) {
+                const size_t pc = p0 + min(c0 + i, nch - 1);
+                ml[i] = *(const float2*)(pml + pc * 2);
+                ov[i] = *(const float4*)(po + pc * HD + d);
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+                if (c0 + i < nch) {
+                    const float f = expf(ml[i].x - M);
+                    den += f * ml[i].y;
+                    acc.x += f * ov[i].x; acc.y += f * ov[i].y; acc.z += f * ov[i].z; acc.w += f * ov[i].w;
+                }
         }
         const float inv = 1.0f / den;
         res = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
@@ -510,6 +577,8 @@ struct AttnArgs {
     int nch_max;
     float *po, *pml;
     hipEvent_t ev0;    // recorded at the start of the first attention kernel (optional)
+    const int32_t* pairs;   // decode work-unit list (attn_pairs_kernel)
+    int n_dec;
 };
 
 template <int HD, int G, int QB>
@@ -539,9 +608,11 @@ static int launch_hd(int G, bool prefill, dim3 grid, hipStream_t s, const AttnAr
 int attn_chunk_size() { return ATT_CHUNK; }
 int attn_prefill_block(int G) { return G > 0 && G <= 32 ? 32 / G : 1; }
 
+// Partials po [T][Hq][nch][HD], pml [T][Hq][nch][2], then the decode
+// work-unit list (1 + T * nch int32).
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos) {
     int nch = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
-    return (size_t)T * Hq * nch * (HD + 2);
+    return (size_t)T * Hq * nch * (HD + 2) + (size_t)T * nch + 1;
 }
 
 // SLATE_HIP_ATTN_WAVE=0 selects the workgroup-phased decode kernel for every shape.
@@ -559,14 +630,15 @@ constexpr int ATT_WAVE_MAX_TOKENS = 64;
 template <int HD, int G>
 static void launch_dec_g(dim3 grid, hipStream_t s, const AttnArgs& a) {
     if constexpr (G * HD <= 512) {
-        if (wave_kernel() && grid.y <= ATT_WAVE_MAX_TOKENS) {
+        if (wave_kernel() && a.n_dec <= ATT_WAVE_MAX_TOKENS) {
             SH_LAUNCH(a.ev0, nullptr, (attn_dec_wave_kernel<HD, G>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp,
-                      a.qt0, a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);
+                      a.qt0, a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml,
+                      a.pairs);
             return;
         }
     }
     SH_LAUNCH(a.ev0, nullptr, (attn_dec_kernel<HD, G>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,
-              a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);
+              a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml, a.pairs);
 }
 
 template <int HD>
@@ -584,7 +656,7 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                            hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop) {
+                            hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool pairs_ready) {
     if (T <= 0) return 0;
     if (Hkv <= 0 || Hq % Hkv != 0) {
         set_error(-1, "attention: n_q_heads %d not a multiple of n_kv_heads %d", Hq, Hkv);
@@ -596,7 +668,13 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
     }
     const int G = Hq / Hkv;
     const int nch_max = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
-    AttnArgs a{q, Kp, Vp, nullptr, nullptr, tok2seq, tok_pos, kv_base, Hq, head_stride, nch_max, po, pml, ev_start};
+    if (n_dec >= 32768 || nch_max > 65536) {
+        set_error(-5, "attention: %d query tokens / %d key chunks exceed the work-unit encoding", n_dec, nch_max);
+        return -5;
+    }
+    int32_t* pairs = (int32_t*)(pml + (size_t)T * Hq * nch_max * 2);
+    AttnArgs a{q, Kp, Vp, nullptr, nullptr, tok2seq, tok_pos, kv_base, Hq, head_stride, nch_max, po, pml, ev_start,
+               pairs, n_dec};
     for (int pass = 0; pass < 2; ++pass) {
         const bool prefill = pass == 1;
         const int nblk = prefill ? n_pre : n_dec;
@@ -606,6 +684,13 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
         dim3 grid(nch_max, nblk, Hkv);
         int rc;
         if (!prefill && (HD == 32 || HD == 64 || HD == 128)) {
+            if (!pairs_ready) {
+                SH_LAUNCH(a.ev0, nullptr, attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos,
+                          nch_max, pairs);
+                SH_CHECK_LAUNCH();
+                a.ev0 = nullptr;
+            }
+            grid = dim3(nch_max * n_dec, 1, Hkv);
             rc = HD == 128 ? launch_dec_hd<128>(G, grid, s, a)
                            : (HD == 64 ? launch_dec_hd<64>(G, grid, s, a) : launch_dec_hd<32>(G, grid, s, a));
         } else {
@@ -638,7 +723,21 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
                             int Hq, int Hkv, int HD, int64_t head_stride, int max_pos, float* po,
                             float* pml, hipStream_t s) {
     return launch_attention_blocks(out, q, Kp, Vp, tok2seq, tok_pos, kv_base, T, nullptr, T, nullptr, nullptr, 0,
-                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s, nullptr, nullptr);
+                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s, nullptr, nullptr, false);
+}
+
+int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, int T, int Hq, int max_pos,
+                           float* pml, hipStream_t s) {
+    const int nch_max = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (n_dec <= 0) return 0;
+    if (n_dec >= 32768 || nch_max > 65536) {
+        set_error(-5, "attention: %d query tokens / %d key chunks exceed the work-unit encoding", n_dec, nch_max);
+        return -5;
+    }
+    hipLaunchKernelGGL(attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, nch_max,
+                       (int32_t*)(pml + (size_t)T * Hq * nch_max * 2));
+    SH_CHECK_LAUNCH();
+    return 0;
 }
 
 // ---------------------------------------------------------------------------

@@ -49,7 +49,13 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                            hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+                            hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr,
+                            bool pairs_ready = false);
+// The decode work-unit list that launch_attention_blocks builds (in the tail
+// of the pml buffer) when pairs_ready is false: build it once when several
+// launches share the same tokens and positions (the layers of one step).
+int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, int T, int Hq, int max_pos,
+                           float* pml, hipStream_t s);
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
 int launch_attention_ragged(float* out, const float* q, const float* Kp, const float* Vp,
                             const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
