@@ -369,3 +369,48 @@ def test_attention_ragged_vs_oracle(hip, orc, hd, Hq, Hkv, extra):
         orc.lib.orc_attention_multihead(fp(want), fp(np.ascontiguousarray(q[t])), fp(Kc), fp(Vc), fp(sc),
                                         L, Hq, Hkv, hd)
         assert np.max(np.abs(got[t] - want)) < 1e-5, (t, L)
+
+
+def test_attention_ragged_full_size_lognormal(hip, orc):
+    """Ragged GQA attention at the full ragged-attention configuration: 64
+    sequences, 32 q / 8 kv heads, head_dim 128, lengths
+    clip(round(exp(N(ln 1024, 1))), 16, 16384) with one sequence at 16384 (64
+    key chunks merged).  K/V (2 x 4.3 GB) are generated on the device; the
+    shortest, the longest and four random sequences are checked against the
+    oracle on the rows they read."""
+    lib = load_library()
+    rng = np.random.default_rng(0xC3)
+    B, Hq, Hkv, hd = 64, 32, 8, 128
+    L = np.clip(np.round(np.exp(rng.normal(np.log(1024.0), 1.0, B))), 16, 16384).astype(np.int64)
+    L[int(rng.integers(B))] = 16384
+    max_seq = int(L.max())
+    head_stride = max_seq * hd
+    slot = Hkv * head_stride
+    Kp, Vp = DB(B * slot * 4), DB(B * slot * 4)
+    check(lib.slate_hip_synth_f32(Kp.p, B * slot, 11, 1.0), "synth K")
+    check(lib.slate_hip_synth_f32(Vp.p, B * slot, 12, 1.0), "synth V")
+    q = rng.normal(0, 1, (B, Hq * hd)).astype(np.float32)
+    out = DB(B * Hq * hd * 4)
+    tok_pos = (L - 1).astype(np.int32)
+    kv_base = np.arange(B, dtype=np.int64) * slot
+    check(lib.slate_hip_attention_ragged(out.p, dev(q).p, Kp.p, Vp.p, dev(np.arange(B, dtype=np.int32)).p,
+                                         dev(tok_pos).p, dev(kv_base).p, B, Hq, Hkv, hd, head_stride, max_seq),
+          "attention_ragged")
+    got = host(out, np.float32, (B, Hq * hd))
+    picks = {int(np.argmin(L)), int(np.argmax(L))} | {int(i) for i in rng.choice(B, 4, replace=False)}
+    for b in sorted(picks):
+        n = int(L[b])
+        Kc = np.empty((Hkv, n, hd), np.float32)
+        Vc = np.empty((Hkv, n, hd), np.float32)
+        for h in range(Hkv):
+            off = (b * slot + h * head_stride) * 4
+            lib.slate_hip_copy_d2h(Kc[h].ctypes.data, C.c_void_p(Kp.ptr + off), n * hd * 4)
+            lib.slate_hip_copy_d2h(Vc[h].ctypes.data, C.c_void_p(Vp.ptr + off), n * hd * 4)
+        Kc = np.ascontiguousarray(Kc.transpose(1, 0, 2).reshape(n, Hkv * hd))
+        Vc = np.ascontiguousarray(Vc.transpose(1, 0, 2).reshape(n, Hkv * hd))
+        want = np.empty(Hq * hd, np.float32)
+        sc = np.empty(n, np.float32)
+        orc.lib.orc_attention_multihead(fp(want), fp(np.ascontiguousarray(q[b])), fp(Kc), fp(Vc), fp(sc),
+                                        n, Hq, Hkv, hd)
+        assert np.all(np.isfinite(got[b]))
+        assert np.max(np.abs(got[b] - want)) < 1e-5, (b, n)
