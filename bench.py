@@ -226,7 +226,8 @@ def main():
         "config": {"workload": "LLaMA-3-8B-shaped Q4_K decode, ragged continuous batching B=16 "
                                "(contexts U[128,2048], stop U[32,256], arrivals with U[64,512]-token prompts)",
                    "layers": args.layers, "d_model": 4096, "heads": "32q/8kv", "ffn": 14336, "vocab": 128256,
-                   "weights": "q4_k", "kv_cache": "f32", "batch": args.batch,
+                   "weights": "q4_k", "kv_cache": "f16" if lib.slate_hip_llama_kv_f16(m.h) == 1 else "f32",
+                   "batch": args.batch,
                    "mixed_prefill_steps": mixed_steps, "arrivals": wl.arrivals - arrivals0,
                    "mean_context_start": round(float(np.mean(ctx0)), 1)},
         "roofline": roofline,

@@ -237,6 +237,12 @@ int   slate_hip_llama_profile(slate_hip_llama_t* m, int enable);
  * Default off: every kernel is launched separately.  Same results either
  * way.  No slate counterpart (slate has no device graphs). */
 int   slate_hip_llama_graphs(slate_hip_llama_t* m, int enable);
+/* 1 when the engine keeps its K/V cache in f16 (opt-in at creation with
+ * SLATE_HIP_KV_F16=1, head_dim 32/64/128), 0 for f32 as the reference
+ * (llama_infer.c:57-58).  f16 halves the attention bytes; it rounds every
+ * cached element to 11 bits, a numerics change measured against the parity
+ * tolerance.  slate_hip_llama_session_kv returns f32 either way. */
+int   slate_hip_llama_kv_f16(const slate_hip_llama_t* m);
 int   slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes,
                                    int64_t* launches);
 

@@ -59,7 +59,9 @@ struct slate_hip_llama {
     float* out_norm = nullptr;
     Lin out;
     std::vector<LayerDev> L;
-    float *Kpool = nullptr, *Vpool = nullptr;
+    void *Kpool = nullptr, *Vpool = nullptr;   // f32, or f16 when kv_f16
+    bool kv_f16 = false;
+    int kv_bytes = 4;
     int64_t slot_stride = 0, layer_stride = 0, head_stride = 0;
     float* rope_cs = nullptr;
     float *x = nullptr, *xn = nullptr, *q = nullptr, *att = nullptr, *h = nullptr;
@@ -148,7 +150,17 @@ int alloc_runtime(slate_hip_llama* m) {
     m->layer_stride = (int64_t)c.n_kv_heads * m->head_stride;
     m->slot_stride = (int64_t)c.n_layers * m->layer_stride;
     size_t kv = (size_t)m->max_slots * m->slot_stride;
-    if (dalloc(m, &m->Kpool, kv) || dalloc(m, &m->Vpool, kv)) return -2;
+    // f16 K/V (opt-in, SLATE_HIP_KV_F16=1): half the attention bytes; the
+    // reference caches f32 (llama_infer.c:57-58)
+    m->kv_f16 = (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) && getenv("SLATE_HIP_KV_F16") != nullptr &&
+                atoi(getenv("SLATE_HIP_KV_F16")) != 0;
+    m->kv_bytes = m->kv_f16 ? 2 : 4;
+    {
+        char *kp = nullptr, *vp = nullptr;
+        if (dalloc(m, &kp, kv * m->kv_bytes) || dalloc(m, &vp, kv * m->kv_bytes)) return -2;
+        m->Kpool = kp;
+        m->Vpool = vp;
+    }
     // RoPE table with the reference's float angle expressions.
     {
         std::vector<float> cs((size_t)c.max_seq * c.head_dim);
@@ -186,7 +198,8 @@ int alloc_runtime(slate_hip_llama* m) {
     // per work unit, whole coalesced K/V rows; the shared prefix re-reads
     // hit L2), which beats the query-block kernel for these head sizes
     m->tokenwise_attn = (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) &&
-                        (getenv("SLATE_HIP_ATTN_TOKENWISE") == nullptr || atoi(getenv("SLATE_HIP_ATTN_TOKENWISE")) != 0);
+                        (m->kv_f16 || getenv("SLATE_HIP_ATTN_TOKENWISE") == nullptr ||
+                         atoi(getenv("SLATE_HIP_ATTN_TOKENWISE")) != 0);
     const int S = m->max_slots;
     const size_t in_ints = 3 * (size_t)S + 4 * T;
     if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
@@ -209,8 +222,8 @@ int alloc_runtime(slate_hip_llama* m) {
     }
     m->h_tok = m->h_desc + 3 * S;
     // KV pools start zeroed, like calloc in llama_infer.c:225-226
-    if (hipMemset(m->Kpool, 0, kv * sizeof(float)) != hipSuccess ||
-        hipMemset(m->Vpool, 0, kv * sizeof(float)) != hipSuccess) {
+    if (hipMemset(m->Kpool, 0, kv * m->kv_bytes) != hipSuccess ||
+        hipMemset(m->Vpool, 0, kv * m->kv_bytes) != hipSuccess) {
         set_error(-7, "engine: KV clear failed");
         return -7;
     }
@@ -460,11 +473,11 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             if (rc) return rc;
             if ((rc = mm_group(m, &a, m->xn, T, D, g, col, 3, D + 2 * kvd, &S, s))) return rc;
         }
-        float* Kl = m->Kpool + (int64_t)li * m->layer_stride;
-        float* Vl = m->Vpool + (int64_t)li * m->layer_stride;
+        char* Kl = (char*)m->Kpool + (int64_t)li * m->layer_stride * m->kv_bytes;
+        char* Vl = (char*)m->Vpool + (int64_t)li * m->layer_stride * m->kv_bytes;
         if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd, m->tok2seq,
                                  m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd, m->head_stride, m->rope_cs,
-                                 rn, s)))
+                                 rn, m->kv_f16, s)))
             return rc;
         {
             const Lin* g[1] = {&Ld.o};
@@ -476,7 +489,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                                               m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
                                               c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
                                               m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea), prof_ev(m, eb),
-                                              true)))
+                                              true, m->kv_f16)))
                 return rc;
             if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
                 m->prof_recs.push_back({m->step_mixed ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, eb});
@@ -914,6 +927,8 @@ int slate_hip_llama_profile(slate_hip_llama_t* m, int enable) {
     return 0;
 }
 
+int slate_hip_llama_kv_f16(const slate_hip_llama_t* m) { return m ? (m->kv_f16 ? 1 : 0) : -1; }
+
 int slate_hip_llama_graphs(slate_hip_llama_t* m, int enable) {
     if (!m) return -1;
     std::lock_guard<std::mutex> lk(m->mu);
@@ -966,11 +981,17 @@ int slate_hip_llama_session_kv(const slate_hip_llama_session_t* s, float* K, flo
     const auto& c = m->cfg;
     const int kvd = c.n_kv_heads * c.head_dim;
     std::vector<float> buf((size_t)m->slot_stride);
+    std::vector<_Float16> hbuf(m->kv_f16 ? (size_t)m->slot_stride : 0);
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
     if (hipStreamSynchronize(stream()) != hipSuccess) return -7;
     for (int which = 0; which < 2; ++which) {
-        const float* src = (which ? m->Vpool : m->Kpool) + (int64_t)s->slot * m->slot_stride;
-        if (hipMemcpy(buf.data(), src, buf.size() * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) return -7;
+        const char* src = (const char*)(which ? m->Vpool : m->Kpool) + (int64_t)s->slot * m->slot_stride * m->kv_bytes;
+        if (m->kv_f16) {
+            if (hipMemcpy(hbuf.data(), src, hbuf.size() * 2, hipMemcpyDeviceToHost) != hipSuccess) return -7;
+            for (size_t i = 0; i < buf.size(); ++i) buf[i] = (float)hbuf[i];
+        } else if (hipMemcpy(buf.data(), src, buf.size() * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) {
+            return -7;
+        }
         float* dst = which ? V : K;
         for (int li = 0; li < c.n_layers; ++li)
             for (int h = 0; h < c.n_kv_heads; ++h)

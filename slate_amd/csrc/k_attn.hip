@@ -210,6 +210,16 @@ __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restr
     if (tid == 0) pairs[0] = s_base;
 }
 
+// Four consecutive K/V elements as floats: f32 caches load 16 bytes, f16
+// caches 8 bytes converted exactly.
+__device__ __forceinline__ float4 ld_kv4(const float* p) { return *(const float4*)p; }
+typedef _Float16 kv_half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ld_kv4(const _Float16* p) {
+    const uint2 r = *(const uint2*)p;
+    const kv_half2_t a = __builtin_bit_cast(kv_half2_t, r.x), b = __builtin_bit_cast(kv_half2_t, r.y);
+    return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+}
+
 // Decode work unit (one query token per sequence): (key chunk, token, kv
 // head), G query heads.  Every K and V row of the chunk is read once, whole
 // and coalesced:
@@ -221,9 +231,9 @@ __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restr
 //   PV      HD/4 lanes per V row (64/(HD/4) rows per wave instruction), the
 //           probabilities broadcast from LDS, reduced over lanes and waves.
 // Partials (chunk max m, sum l, unnormalised output) as attn_block_kernel.
-template <int HD, int G>
+template <int HD, int G, typename KVT>
 __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
-    const float* __restrict__ q, const float* __restrict__ Kp, const float* __restrict__ Vp,
+    const float* __restrict__ q, const KVT* __restrict__ Kp, const KVT* __restrict__ Vp,
     const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
     const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
     float* __restrict__ pml, const int32_t* __restrict__ pairs) {
@@ -247,8 +257,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     const int lg = lane >> 3, ls = lane & 7;
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t base = kv_base[tok2seq[t]] + (int64_t)h * head_stride + (int64_t)k0 * HD;
-    const float* Kh = Kp + base;
-    const float* Vh = Vp + base;
+    const KVT* Kh = Kp + base;
+    const KVT* Vh = Vp + base;
     const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
     float4 qv[G][NV];
 #pragma unroll
@@ -260,10 +270,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
 #pragma unroll 2
     for (int j0 = 0; j0 < nkp; j0 += 32) {
         const int j = j0 + 8 * wv + lg;
-        const float* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
+        const KVT* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
         float4 kv[NV];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) kv[i] = *(const float4*)(kr + 32 * i + 4 * ls);
+        for (int i = 0; i < NV; ++i) kv[i] = ld_kv4(kr + 32 * i + 4 * ls);
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             float a = 0.f;
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     for (int gi = 0; gi < G; ++gi) acc[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 4
     for (int j = wv * KPI + kof; j < nkp; j += 4 * KPI) {
-        const float4 vv = *(const float4*)(Vh + (int64_t)min(j, nk - 1) * HD + 4 * d4);
+        const float4 vv = ld_kv4(Vh + (int64_t)min(j, nk - 1) * HD + 4 * d4);
 #pragma unroll
         for (int gi = 0; gi < G; ++gi) {
             const float pj = sp[gi][j];
@@ -354,9 +364,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
 // The waves then combine through LDS (log-sum-exp over the four wave
 // maxima) into the chunk partial (max m, sum l, unnormalised output), as
 // attn_block_kernel writes it.
-template <int HD, int G>
+template <int HD, int G, typename KVT>
 __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
-    const float* __restrict__ q, const float* __restrict__ Kp, const float* __restrict__ Vp,
+    const float* __restrict__ q, const KVT* __restrict__ Kp, const KVT* __restrict__ Vp,
     const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
     const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
     float* __restrict__ pml, const int32_t* __restrict__ pairs) {
@@ -379,8 +389,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
     const int lg = lane >> 3, ls = lane & 7;
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t base = kv_base[tok2seq[t]] + (int64_t)h * head_stride + (int64_t)k0 * HD;
-    const float* Kh = Kp + base;
-    const float* Vh = Vp + base;
+    const KVT* Kh = Kp + base;
+    const KVT* Vh = Vp + base;
     const int kw0 = wv * KW;
     if (kw0 < nk) {
         const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
@@ -393,10 +403,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int j = kw0 + 8 * it + lg;
-            const float* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
+            const KVT* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
             float4 kv[NV];
 #pragma unroll
-            for (int i = 0; i < NV; ++i) kv[i] = *(const float4*)(kr + 32 * i + 4 * ls);
+            for (int i = 0; i < NV; ++i) kv[i] = ld_kv4(kr + 32 * i + 4 * ls);
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 float a = 0.f;
@@ -417,9 +427,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
         float4 vpre[VP][NV];
 #pragma unroll
         for (int it = 0; it < VP; ++it) {
-            const float* vr = Vh + (int64_t)min(kw0 + 8 * it + lg, nk - 1) * HD;
+            const KVT* vr = Vh + (int64_t)min(kw0 + 8 * it + lg, nk - 1) * HD;
 #pragma unroll
-            for (int i = 0; i < NV; ++i) vpre[it][i] = *(const float4*)(vr + 32 * i + 4 * ls);
+            for (int i = 0; i < NV; ++i) vpre[it][i] = ld_kv4(vr + 32 * i + 4 * ls);
         }
         __builtin_amdgcn_sched_barrier(0);
         float mx[G], sum[G];
@@ -446,10 +456,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int j = kw0 + 8 * it + lg;
-            const float* vr = Vh + (int64_t)min(j, nk - 1) * HD;
+            const KVT* vr = Vh + (int64_t)min(j, nk - 1) * HD;
             float4 vv[NV];
 #pragma unroll
-            for (int i = 0; i < NV; ++i) vv[i] = it < VP ? vpre[it][i] : *(const float4*)(vr + 32 * i + 4 * ls);
+            for (int i = 0; i < NV; ++i) vv[i] = it < VP ? vpre[it][i] : ld_kv4(vr + 32 * i + 4 * ls);
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 const float pj = sc[gi][it];
@@ -569,7 +579,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
 }
 
 struct AttnArgs {
-    const float *q, *Kp, *Vp;
+    const float* q;
+    const void *Kp, *Vp;      // f32 or f16 (kv_f16) caches
     const int32_t *qt0, *qn, *tok2seq, *tok_pos;
     const int64_t* kv_base;
     int Hq;
@@ -579,11 +590,13 @@ struct AttnArgs {
     hipEvent_t ev0;    // recorded at the start of the first attention kernel (optional)
     const int32_t* pairs;   // decode work-unit list (attn_pairs_kernel)
     int n_dec;
+    bool kv_f16;
 };
 
 template <int HD, int G, int QB>
 static void launch_blk(dim3 grid, hipStream_t s, const AttnArgs& a) {
-    SH_LAUNCH(a.ev0, nullptr, (attn_block_kernel<HD, G, QB>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,
+    SH_LAUNCH(a.ev0, nullptr, (attn_block_kernel<HD, G, QB>), grid, dim3(ATT_THREADS), 0, s, a.q,
+              (const float*)a.Kp, (const float*)a.Vp, a.qt0,
                        a.qn, a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml);
 }
 
@@ -627,18 +640,26 @@ static bool wave_kernel() {
 // its higher occupancy.
 constexpr int ATT_WAVE_MAX_TOKENS = 64;
 
-template <int HD, int G>
-static void launch_dec_g(dim3 grid, hipStream_t s, const AttnArgs& a) {
+template <int HD, int G, typename KVT>
+static void launch_dec_t(dim3 grid, hipStream_t s, const AttnArgs& a) {
+    const KVT* Kp = (const KVT*)a.Kp;
+    const KVT* Vp = (const KVT*)a.Vp;
     if constexpr (G * HD <= 512) {
         if (wave_kernel() && a.n_dec <= ATT_WAVE_MAX_TOKENS) {
-            SH_LAUNCH(a.ev0, nullptr, (attn_dec_wave_kernel<HD, G>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp,
+            SH_LAUNCH(a.ev0, nullptr, (attn_dec_wave_kernel<HD, G, KVT>), grid, dim3(ATT_THREADS), 0, s, a.q, Kp, Vp,
                       a.qt0, a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml,
                       a.pairs);
             return;
         }
     }
-    SH_LAUNCH(a.ev0, nullptr, (attn_dec_kernel<HD, G>), grid, dim3(ATT_THREADS), 0, s, a.q, a.Kp, a.Vp, a.qt0,
+    SH_LAUNCH(a.ev0, nullptr, (attn_dec_kernel<HD, G, KVT>), grid, dim3(ATT_THREADS), 0, s, a.q, Kp, Vp, a.qt0,
               a.tok2seq, a.tok_pos, a.kv_base, a.Hq, a.head_stride, a.nch_max, a.po, a.pml, a.pairs);
+}
+
+template <int HD, int G>
+static void launch_dec_g(dim3 grid, hipStream_t s, const AttnArgs& a) {
+    if (a.kv_f16) launch_dec_t<HD, G, _Float16>(grid, s, a);
+    else launch_dec_t<HD, G, float>(grid, s, a);
 }
 
 template <int HD>
@@ -652,12 +673,17 @@ static int launch_dec_hd(int G, dim3 grid, hipStream_t s, const AttnArgs& a) {
     }
 }
 
-int launch_attention_blocks(float* out, const float* q, const float* Kp, const float* Vp, const int32_t* tok2seq,
+int launch_attention_blocks(float* out, const float* q, const void* Kp, const void* Vp, const int32_t* tok2seq,
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                            hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool pairs_ready) {
+                            hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool pairs_ready,
+                            bool kv_f16) {
     if (T <= 0) return 0;
+    if (kv_f16 && (n_pre > 0 || !(HD == 32 || HD == 64 || HD == 128))) {
+        set_error(-5, "attention: f16 K/V caches need head_dim 32, 64 or 128 and one work unit per token");
+        return -5;
+    }
     if (Hkv <= 0 || Hq % Hkv != 0) {
         set_error(-1, "attention: n_q_heads %d not a multiple of n_kv_heads %d", Hq, Hkv);
         return -1;
@@ -674,7 +700,7 @@ int launch_attention_blocks(float* out, const float* q, const float* Kp, const f
     }
     int32_t* pairs = (int32_t*)(pml + (size_t)T * Hq * nch_max * 2);
     AttnArgs a{q, Kp, Vp, nullptr, nullptr, tok2seq, tok_pos, kv_base, Hq, head_stride, nch_max, po, pml, ev_start,
-               pairs, n_dec};
+               pairs, n_dec, kv_f16};
     for (int pass = 0; pass < 2; ++pass) {
         const bool prefill = pass == 1;
         const int nblk = prefill ? n_pre : n_dec;
@@ -723,7 +749,8 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
                             int Hq, int Hkv, int HD, int64_t head_stride, int max_pos, float* po,
                             float* pml, hipStream_t s) {
     return launch_attention_blocks(out, q, Kp, Vp, tok2seq, tok_pos, kv_base, T, nullptr, T, nullptr, nullptr, 0,
-                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s, nullptr, nullptr, false);
+                                   Hq, Hkv, HD, head_stride, max_pos, po, pml, nullptr, s, nullptr, nullptr, false,
+                                   false);
 }
 
 int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, int T, int Hq, int max_pos,

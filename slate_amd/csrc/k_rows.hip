@@ -347,8 +347,9 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
 // QKV epilogue, one wave per (token, head): sums the split-K partials of the
 // head's columns, rotates q / k at the token's position (same table and
 // expressions as rope_apply) and writes q to qout, k and v into the KV pool.
-__global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, float* __restrict__ Kpool,
-                                                     float* __restrict__ Vpool, const float* __restrict__ part,
+template <typename KVT>
+__global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, KVT* __restrict__ Kpool,
+                                                     KVT* __restrict__ Vpool, const float* __restrict__ part,
                                                      int nsplit, int64_t split_stride, int qkv_ld,
                                                      const int32_t* __restrict__ tok2seq,
                                                      const int32_t* __restrict__ tok_pos,
@@ -385,22 +386,27 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, f
             const float a = col(ck), b = col(ck + half);
             const float c = cs[((size_t)ap * half + i) * 2 + 0];
             const float sn = sg * cs[((size_t)ap * half + i) * 2 + 1];
-            Kpool[base + i] = a * c - b * sn;
-            Kpool[base + i + half] = a * sn + b * c;
-            Vpool[base + i] = col(cv);
-            Vpool[base + i + half] = col(cv + half);
+            Kpool[base + i] = (KVT)(a * c - b * sn);
+            Kpool[base + i + half] = (KVT)(a * sn + b * c);
+            Vpool[base + i] = (KVT)col(cv);
+            Vpool[base + i + half] = (KVT)col(cv + half);
         }
     }
 }
 
-int launch_rope_kv(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit, int64_t split_stride,
+int launch_rope_kv(float* qout, void* Kpool, void* Vpool, const float* part, int nsplit, int64_t split_stride,
                    int qkv_ld, const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
                    int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, const RowNorm& rn,
-                   hipStream_t s) {
+                   bool kv_f16, hipStream_t s) {
     if (T <= 0) return 0;
-    hipLaunchKernelGGL(rope_kv_kernel, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout, Kpool, Vpool, part,
-                       nsplit, split_stride, qkv_ld, tok2seq, tok_pos, kv_base, n_heads, n_kv_heads, hd,
-                       head_stride, cs, rn);
+    if (kv_f16)
+        hipLaunchKernelGGL(rope_kv_kernel<_Float16>, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout,
+                           (_Float16*)Kpool, (_Float16*)Vpool, part, nsplit, split_stride, qkv_ld, tok2seq, tok_pos,
+                           kv_base, n_heads, n_kv_heads, hd, head_stride, cs, rn);
+    else
+        hipLaunchKernelGGL(rope_kv_kernel<float>, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout,
+                           (float*)Kpool, (float*)Vpool, part, nsplit, split_stride, qkv_ld, tok2seq, tok_pos,
+                           kv_base, n_heads, n_kv_heads, hd, head_stride, cs, rn);
     SH_CHECK_LAUNCH();
     return 0;
 }

@@ -22,10 +22,11 @@ int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64
                        int rows, int D, float eps, const Act16* a, hipStream_t s);
 int launch_silu_act(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
                     int64_t split_stride, int64_t ld, const Act16* a, const RowNorm& rn, hipStream_t s);
-int launch_rope_kv(float* qout, float* Kpool, float* Vpool, const float* part, int nsplit, int64_t split_stride,
+// K/V rows are written as f32, or rounded to f16 when kv_f16.
+int launch_rope_kv(float* qout, void* Kpool, void* Vpool, const float* part, int nsplit, int64_t split_stride,
                    int qkv_ld, const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
                    int n_heads, int n_kv_heads, int hd, int64_t head_stride, const float* cs, const RowNorm& rn,
-                   hipStream_t s);
+                   bool kv_f16, hipStream_t s);
 // x += sum of split partials, per-block sums of squares into ssq, x * w as
 // the Q4_K operand (the row factor is left to the consumer, RowNorm).
 int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_stride, const float* w, int rows,
@@ -45,12 +46,12 @@ int attn_prefill_block(int group);   // query tokens per block for prompt chunks
 // consecutive tokens of one sequence.  Every token must be covered once.
 // `act` (nullable) also receives the output rows as the Q4_K activation
 // operand (Hq * HD % 256 == 0).
-int launch_attention_blocks(float* out, const float* q, const float* Kp, const float* Vp, const int32_t* tok2seq,
+int launch_attention_blocks(float* out, const float* q, const void* Kp, const void* Vp, const int32_t* tok2seq,
                             const int32_t* tok_pos, const int64_t* kv_base, int T, const int32_t* dec_t0,
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
                             hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr,
-                            bool pairs_ready = false);
+                            bool pairs_ready = false, bool kv_f16 = false);
 // The decode work-unit list that launch_attention_blocks builds (in the tail
 // of the pml buffer) when pairs_ready is false: build it once when several
 // launches share the same tokens and positions (the layers of one step).

@@ -280,3 +280,60 @@ def test_graph_replayed_decode_steps_match_eager_launches(golden):
         assert np.array_equal(la, lb) and np.array_equal(na, nb)
     for (K1, V1), (K2, V2) in zip(akv, bkv):
         assert np.array_equal(K1, K2) and np.array_equal(V1, V2)
+
+
+def test_f16_kv_cache_tolerance_study(orc, monkeypatch):
+    """The opt-in f16 K/V cache against the oracle's f32 reference: a 512-wide
+    Q4_K model (head_dim 64), three prompts of 150-280 tokens (contexts over
+    two 256-key chunks), 24 ragged decode steps; every step's logits stay
+    within the parity tolerance (normwise relative 1e-3).  Layer 0's cached
+    K/V equal the f32 engine's rounded to f16 (layers above also carry the
+    f16 attention's own rounding)."""
+    shape = LlamaShape(2, 512, 8, 4, 768, 300, 512)
+    t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(16)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (150, 220, 280)]
+    engines = {}
+    for f16 in (True, False):
+        monkeypatch.setenv("SLATE_HIP_KV_F16", "1" if f16 else "0")
+        m = slate_amd.Llama.from_tensors(shape, t, max_slots=4, max_tokens=1024)
+        assert m.lib.slate_hip_llama_kv_f16(m.h) == (1 if f16 else 0)
+        sess = [m.session() for _ in prompts]
+        rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+        assert rc == 0
+        steps = [lg]
+        toks = np.asarray(nxt, np.int32)
+        for _ in range(24):
+            rc, lg, nxt = m.step(sess, [1, 1, 1], toks)
+            assert rc == 0
+            steps.append(lg)
+            toks = np.asarray(nxt, np.int32)
+        engines[f16] = (m, sess, steps)
+    m16, s16, steps16 = engines[True]
+    m32, s32, steps32 = engines[False]
+    om = OracleModel(orc, shape, t)
+    worst = 0.0
+    for i, p in enumerate(prompts):
+        o = om.session()
+        rc, want = o.prefill(p)
+        assert rc == 0
+        worst = max(worst, relerr(steps16[0][i], want))
+        tok = int(np.argmax(steps16[0][i]))
+        for k in range(1, len(steps16)):
+            rc, want = o.decode(tok)
+            assert rc == 0
+            e = relerr(steps16[k][i], want)
+            worst = max(worst, e)
+            assert e < TOL, (i, k, e)
+            tok = int(np.argmax(steps16[k][i]))
+    print(f"f16 K/V: worst normwise logits error vs the f32 reference {worst:.2e}")
+    for a, b in zip(s16, s32):
+        (K16, V16), (K32, V32) = a.kv(), b.kv()
+        n = a.position
+        for X16, X32 in ((K16, K32), (V16, V32)):
+            ref = X32[0, :n].astype(np.float16).astype(np.float32)
+            assert np.array_equal(X16[0, :n], ref)
+    for m, sess, _ in engines.values():
+        for s in sess:
+            s.free()
+        m.free()
