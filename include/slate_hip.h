@@ -112,6 +112,24 @@ int   slate_hip_dequant_q4k(float* dst, const void* A_q4k, int64_t n);
 int64_t slate_hip_q4k_tiled_bytes(int M, int K);
 int   slate_hip_q4k_tile(void* dst_tiled, const void* src_q4k, int M, int K);
 int   slate_hip_matmul_q4k_tiled(float* Y, const void* A_tiled, const float* X, int B, int M, int K);
+/* Q8_0 (34-byte blocks [f16 d][32 x int8], quant.h:16-31), device pointers.
+ * q8_0_matvec has slate_q8_0_matvec's signature and meaning (quant.c:126-133,
+ * y[m] = sum_k d*q[m,k] * x[k], K % 32 == 0); matmul_q8_0 is B such calls in
+ * one launch (Y[B,M] = X[B,K] @ dequant(A)[M,K]^T); dequant_q8_0 is
+ * slate_dequant_q8_0 (quant.c:12-25), bit-exact, n % 32 == 0.  Sums are in
+ * another order than the reference's eight AVX2 lanes (float tolerance). */
+void  slate_hip_q8_0_matvec(float* y, const void* A_q8, const float* x, int M, int K);  /* quant.h:31 */
+int   slate_hip_matmul_q8_0(float* Y, const void* A_q8, const float* X, int B, int M, int K);
+int   slate_hip_dequant_q8_0(float* dst, const void* A_q8, int64_t n);                   /* quant.h:24 */
+/* Tiled Q8_0: the same bytes regrouped into 16-row x 256-element tiles of
+ * 4352 bytes (the eight d of each row, then the int8 weights in the order
+ * the matmul lanes read them); rows past M and blocks past K/32 are zero.
+ * matmul_q8_0 regroups into backend scratch on every call; callers that
+ * keep weights resident tile them once with q8_0_tile (device src, row
+ * layout, into dst of q8_0_tiled_bytes) and call matmul_q8_0_tiled. */
+int64_t slate_hip_q8_0_tiled_bytes(int M, int K);
+int   slate_hip_q8_0_tile(void* dst_tiled, const void* src_q8, int M, int K);
+int   slate_hip_matmul_q8_0_tiled(float* Y, const void* A_tiled, const float* X, int B, int M, int K);
 int   slate_hip_rmsnorm_rows(float* y, const float* x, const float* w, int B, int D, float eps);
 /* RoPE with the angles of llama_infer.c:83-86 (host powf/cosf/sinf table,
  * so identical inputs rotate bit-identically); rows with |pos| >= max_pos
@@ -161,7 +179,9 @@ typedef struct slate_hip_llama_config {
 } slate_hip_llama_config_t;
 
 /* Mirrors slate_llama_layer_t (llama.h:69-86): host pointers, dtypes are
- * slate_dtype_t values (0 = F32, 18 = Q4_K). */
+ * slate_dtype_t values (0 = F32, 16 = Q8_0, 18 = Q4_K).  Unlike the
+ * reference's mv_dispatch (llama_infer.c:43-51), which reads a Q8_0 tensor
+ * as f32, Q8_0 linears run the Q8_0 matmul. */
 typedef struct slate_hip_llama_layer {
     const void *attn_norm, *attn_q, *attn_k, *attn_v, *attn_output;
     const void *ffn_norm, *ffn_gate, *ffn_up, *ffn_down;
@@ -181,7 +201,8 @@ slate_hip_llama_t* slate_hip_llama_new(const slate_hip_llama_config_t* cfg,
                                        const slate_hip_llama_layer_t* layers,
                                        int max_slots, int max_tokens);
 /* Same engine with seeded synthetic weights generated on the device:
- * linears Q4_K (quant = 18) or F32 (quant = 0), embeddings f32, norms 1. */
+ * linears Q4_K (quant = 18), Q8_0 (quant = 16) or F32 (quant = 0),
+ * embeddings f32, norms 1. */
 slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t* cfg,
                                                  uint64_t seed, int quant,
                                                  int max_slots, int max_tokens);

@@ -143,6 +143,54 @@ void orc_q4k_matmul(float* Y, const void* A, const float* X, int B, int M, int K
 }
 
 /* ------------------------------------------------------------------------ */
+/* quant.c:12-25 -- Q8_0 block: [f16 d][32 x int8 q]; w = d * (float)q. */
+void orc_dequant_q8_0(float* dst, const void* src, int64_t n) {
+    const uint8_t* p = (const uint8_t*)src;
+    for (int64_t b = 0; b < n / ORC_Q8_0_BLOCK_ELEMS; ++b) {
+        const uint8_t* blk = p + b * ORC_Q8_0_BLOCK_BYTES;
+        uint16_t h;
+        memcpy(&h, blk, 2);
+        const float d = orc_f16_to_f32(h);
+        const int8_t* q = (const int8_t*)(blk + 2);
+        for (int i = 0; i < ORC_Q8_0_BLOCK_ELEMS; ++i) dst[b * ORC_Q8_0_BLOCK_ELEMS + i] = d * (float)q[i];
+    }
+}
+
+/* quant.c:64-109, AVX2 branch (the one the reference build runs): lane l of
+ * one 8-wide accumulator takes, per block in order, fma(d*q[i], x[i], acc)
+ * for i = l, 8+l, 16+l, 24+l; the eight lanes are then added left to right
+ * into a float that starts at 0. */
+float orc_dot_q8_0_f32(const void* blocks, const float* x, int64_t n) {
+    const uint8_t* p = (const uint8_t*)blocks;
+    float acc[8] = {0};
+    for (int64_t b = 0; b < n / ORC_Q8_0_BLOCK_ELEMS; ++b) {
+        const uint8_t* blk = p + b * ORC_Q8_0_BLOCK_BYTES;
+        uint16_t h;
+        memcpy(&h, blk, 2);
+        const float d = orc_f16_to_f32(h);
+        const int8_t* q = (const int8_t*)(blk + 2);
+        const float* xb = x + b * ORC_Q8_0_BLOCK_ELEMS;
+        for (int r = 0; r < 4; ++r)
+            for (int l = 0; l < 8; ++l) acc[l] = fmaf(d * (float)q[8 * r + l], xb[8 * r + l], acc[l]);
+    }
+    float total = 0.0f;
+    for (int l = 0; l < 8; ++l) total += acc[l];
+    return total;
+}
+
+/* quant.c:126-133 -- row stride K/32 * 34 bytes. */
+void orc_q8_0_matvec(float* y, const void* A, const float* x, int M, int K) {
+    size_t row_bytes = (size_t)(K / ORC_Q8_0_BLOCK_ELEMS) * ORC_Q8_0_BLOCK_BYTES;
+    for (int m = 0; m < M; ++m)
+        y[m] = orc_dot_q8_0_f32((const uint8_t*)A + (size_t)m * row_bytes, x, K);
+}
+
+void orc_q8_0_matmul(float* Y, const void* A, const float* X, int B, int M, int K) {
+    for (int b = 0; b < B; ++b)
+        orc_q8_0_matvec(Y + (size_t)b * M, A, X + (size_t)b * K, M, K);
+}
+
+/* ------------------------------------------------------------------------ */
 /* matmul.c:158-199 with the 8x16 microkernel (:85-134): every C element is a
  * sum over KC=128 slices; inside a slice a zero-started fma chain, and each
  * slice's chain is then added to C in ascending slice order.  Blocking over
@@ -405,10 +453,14 @@ void orc_session_kv(const orc_session* s, float* K_out, float* V_out) {
     memcpy(V_out, s->V, n * sizeof(float));
 }
 
-/* llama_infer.c:43-51 -- dtype 18 (Q4_K) takes the Q4_K matvec, anything
- * else is read as f32. */
+/* llama_infer.c:43-51 -- dtype 18 (Q4_K) takes the Q4_K matvec and f32 the
+ * f32 one.  Dtype 16 (Q8_0) is where this restatement departs on purpose:
+ * the reference reads a Q8_0 tensor's bytes as f32 (its dispatch knows only
+ * 18), which is a bug, so here it takes quant.c:126-133 -- the corrected
+ * dispatch that the HIP engine implements. */
 static void mv(float* y, const void* W, int dtype, const float* x, int M, int K) {
     if (dtype == 18) orc_q4k_matvec(y, W, x, M, K);
+    else if (dtype == 16) orc_q8_0_matvec(y, W, x, M, K);
     else orc_matvec(y, (const float*)W, x, M, K);
 }
 

@@ -39,6 +39,18 @@ void     orc_q4k_matvec(float* y, const void* A, const float* x,
 void     orc_q4k_matmul(float* Y, const void* A, const float* X,
                         int B, int M, int K);
 
+/* ---- Q8_0 (include/slate/quant.h:16-31) --------------------------------- */
+#define ORC_Q8_0_BLOCK_BYTES 34
+#define ORC_Q8_0_BLOCK_ELEMS 32
+void     orc_dequant_q8_0(float* dst, const void* src, int64_t n); /* quant.c:12-25 */
+float    orc_dot_q8_0_f32(const void* blocks, const float* x,
+                          int64_t n);                              /* quant.c:64-109 */
+void     orc_q8_0_matvec(float* y, const void* A, const float* x,
+                         int M, int K);                            /* quant.c:126-133 */
+/* B independent calls of quant.c:126-133. */
+void     orc_q8_0_matmul(float* Y, const void* A, const float* X,
+                         int B, int M, int K);
+
 /* ---- f32 GEMM behind the vtable ---------------------------------------- */
 /* C[M,N] += A[M,K] @ B[K,N]; KC=128 blocked fma chains, matmul.c:36-199 */
 void     orc_gemm_accumulate(float* C, int64_t ldc, const float* A, int64_t lda,

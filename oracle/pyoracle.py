@@ -80,6 +80,9 @@ class Oracle:
         _sig(L, "orc_dot_q4k_f32", C.c_float, vp, f32p, C.c_int64)
         _sig(L, "orc_q4k_matvec", None, f32p, vp, f32p, C.c_int, C.c_int)
         _sig(L, "orc_q4k_matmul", None, f32p, vp, f32p, C.c_int, C.c_int, C.c_int)
+        _sig(L, "orc_dequant_q8_0", None, f32p, vp, C.c_int64)
+        _sig(L, "orc_dot_q8_0_f32", C.c_float, vp, f32p, C.c_int64)
+        _sig(L, "orc_q8_0_matmul", None, f32p, vp, f32p, C.c_int, C.c_int, C.c_int)
         _sig(L, "orc_matvec", None, f32p, f32p, f32p, C.c_int, C.c_int)
         _sig(L, "orc_linear_batch", None, f32p, f32p, f32p, C.c_int, C.c_int, C.c_int)
         _sig(L, "orc_rmsnorm_row", None, f32p, f32p, f32p, C.c_int, C.c_float)
@@ -112,6 +115,19 @@ class Oracle:
         X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
         Y = np.empty((X.shape[0], M), np.float32)
         self.lib.orc_q4k_matmul(fp(Y), bp(raw), fp(X), X.shape[0], M, K)
+        return Y
+
+    def dequant_q8_0(self, raw, n):
+        raw = np.ascontiguousarray(np.frombuffer(bytes(raw), np.uint8))
+        out = np.empty(n, np.float32)
+        self.lib.orc_dequant_q8_0(fp(out), bp(raw), n)
+        return out
+
+    def q8_0_matmul(self, raw, X, M, K):
+        raw = np.ascontiguousarray(np.frombuffer(bytes(raw), np.uint8)) if not isinstance(raw, np.ndarray) else raw
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, K)
+        Y = np.empty((X.shape[0], M), np.float32)
+        self.lib.orc_q8_0_matmul(fp(Y), bp(raw), fp(X), X.shape[0], M, K)
         return Y
 
     def pack_batch(self, slot, pos0, n_new, max_seq, slot_stride):
@@ -212,6 +228,9 @@ class Ref:
         _sig(L, "slate_dequant_q4_k", None, f32p, vp, C.c_int64)
         _sig(L, "slate_dot_q4_k_f32", C.c_float, vp, f32p, C.c_int64)
         _sig(L, "slate_q4_k_matvec", None, f32p, vp, f32p, C.c_int, C.c_int)
+        _sig(L, "slate_dequant_q8_0", None, f32p, vp, C.c_int64)
+        _sig(L, "slate_dot_q8_0_f32", C.c_float, vp, f32p, C.c_int64)
+        _sig(L, "slate_q8_0_matvec", None, f32p, vp, f32p, C.c_int, C.c_int)
         _sig(L, "ref_rope_inplace_row", None, f32p, C.c_int, C.c_int, C.c_int, C.c_float)
         _sig(L, "ref_attention_multihead", None, f32p, f32p, f32p, f32p, f32p,
              C.c_int, C.c_int, C.c_int, C.c_int)

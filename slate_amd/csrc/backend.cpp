@@ -131,6 +131,15 @@ int make_act16(Act16& a, int B, int K, int slot) {
     return a.frag ? 0 : -2;
 }
 
+// Activation operand buffer for one Q8_0 matmul input of B rows x K.
+int make_act8(Act8& a, int B, int K, int slot) {
+    a.rows = B;
+    a.rows_pad = row_pad(B);
+    a.K = K;
+    a.frag = scratch(slot, act8_bytes(a.rows_pad, K));
+    return a.frag ? 0 : -2;
+}
+
 }  // namespace slate_hip
 
 using namespace slate_hip;
@@ -252,6 +261,63 @@ int slate_hip_dequant_q4k(float* dst, const void* A, int64_t n) {
     SH_REQUIRE(dst && A && n >= 0 && n % QK == 0, "dequant_q4k: bad arguments");
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
     return launch_dequant_q4k(dst, A, n / QK, g_stream);
+}
+
+static int matmul_q8_common(float* Y, const void* A, const float* X, int B, int M, int K, bool tiled) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(Y && A && X && B > 0 && M > 0 && K > 0, "matmul_q8_0: bad arguments");
+    SH_REQUIRE(K % Q8_ELEMS == 0, "matmul_q8_0: K=%d is not a multiple of 32", K);
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    const void* W = A;
+    int rc;
+    if (!tiled) {   // regroup the row layout into the matmul's tiles first
+        void* t = scratch(5, q8_tiled_bytes(M, K));
+        if (!t) return -2;
+        if ((rc = launch_q8_tile(t, A, M, K, g_stream))) return rc;
+        W = t;
+    }
+    Act8 a;
+    if (make_act8(a, B, K, 4)) return -2;
+    if ((rc = launch_act8_from_f32(a, X, K, g_stream))) return rc;
+    const int max_splits = 32;
+    float* part = (float*)scratch(1, (size_t)max_splits * a.rows_pad * M * sizeof(float));
+    if (!part) return -2;
+    Q4kTarget t{W, M, 0};
+    int S = 1;
+    rc = launch_q8(&t, 1, a, part, (int64_t)M, (int64_t)a.rows_pad * M, max_splits, 0, &S, g_stream);
+    if (rc) return rc;
+    return launch_sum_splits(Y, part, S, B, a.rows_pad, M, g_stream);
+}
+
+int slate_hip_matmul_q8_0(float* Y, const void* A, const float* X, int B, int M, int K) {
+    return matmul_q8_common(Y, A, X, B, M, K, false);
+}
+
+int slate_hip_matmul_q8_0_tiled(float* Y, const void* A, const float* X, int B, int M, int K) {
+    return matmul_q8_common(Y, A, X, B, M, K, true);
+}
+
+void slate_hip_q8_0_matvec(float* y, const void* A, const float* x, int M, int K) {
+    slate_hip_matmul_q8_0(y, A, x, 1, M, K);
+}
+
+int64_t slate_hip_q8_0_tiled_bytes(int M, int K) {
+    if (M <= 0 || K <= 0 || K % Q8_ELEMS) return -1;
+    return (int64_t)q8_tiled_bytes(M, K);
+}
+
+int slate_hip_q8_0_tile(void* dst, const void* src, int M, int K) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(dst && src && M > 0 && K > 0 && K % Q8_ELEMS == 0, "q8_0_tile: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_q8_tile(dst, src, M, K, g_stream);
+}
+
+int slate_hip_dequant_q8_0(float* dst, const void* A, int64_t n) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(dst && A && n >= 0 && n % Q8_ELEMS == 0, "dequant_q8_0: bad arguments");
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    return launch_dequant_q8(dst, A, n / Q8_ELEMS, g_stream);
 }
 
 int slate_hip_rmsnorm_rows(float* y, const float* x, const float* w, int B, int D, float eps) {

@@ -113,4 +113,42 @@ inline int row_pad(int rows) { return rows <= 64 ? (rows + 15) / 16 * 16 : (rows
 // Carve an Act16 for B rows x K out of backend scratch slot `slot`.
 int make_act16(Act16& a, int B, int K, int slot);
 
+// ---------------------------------------------------------------------------
+// Q8_0 (include/slate/quant.h:16-31): 34-byte blocks of [f16 d][32 x int8].
+constexpr int Q8_ELEMS = 32;
+constexpr int Q8_BYTES = 34;
+// TILED Q8_0 layout (k_q8.hip): 16-row tiles x 256-element groups of 4352
+// bytes; K is padded to whole groups with zero blocks.
+constexpr int Q8_GROUP = 256;
+constexpr int Q8_TB = 4352;
+__host__ __device__ inline int q8_groups(int K) { return (K + Q8_GROUP - 1) / Q8_GROUP; }
+size_t q8_tiled_bytes(int M, int K);
+int launch_q8_tile(void* dst, const void* src, int M, int K, hipStream_t s);
+void q8_untile_host(uint8_t* dst, const uint8_t* src, int M, int K);
+int launch_dequant_q8(float* dst, const void* src, int64_t n_blocks, hipStream_t s);
+
+// Activation operand of the Q8_0 matmul: like Act16 (f16 hi + lo with a
+// power-of-two scale per 256-element group and row) but with the elements of
+// each MFMA K step inside one 32-element Q8_0 block, and no sums:
+// frag [rows_pad/16][q8_groups(K)][ACT8_UNITS] 16-byte units.
+constexpr int ACT8_UNITS = 1088;           // 1028 used, padded to 17 x 64
+struct Act8 {
+    void* frag;
+    int rows;       // valid rows
+    int rows_pad;   // multiple of 16
+    int K;          // multiple of 32
+};
+inline size_t act8_bytes(int rows_pad, int K) {
+    return (size_t)(rows_pad / 16) * q8_groups(K) * ACT8_UNITS * 16;
+}
+int launch_act8_from_f32(const Act8& a, const float* X, int64_t ldx, hipStream_t s);
+int make_act8(Act8& a, int B, int K, int slot);
+// Up to three TILED Q8_0 tensors sharing one input (targets and partial
+// layout as launch_q4k).  fixed_splits > 0 forces that split count (a group
+// that also holds Q4_K tensors must write the same partials); otherwise the
+// count is chosen (<= max_splits) and returned in *S_out.
+int launch_q8(const Q4kTarget* t, int n, const Act8& a, float* out, int64_t ldo, int64_t split_stride,
+              int max_splits, int fixed_splits, int* S_out, hipStream_t s, hipEvent_t ev_start = nullptr,
+              hipEvent_t ev_stop = nullptr);
+
 }  // namespace slate_hip

@@ -7,7 +7,8 @@
 // HBM layout:
 //   weights       Q4_K in the TILED layout (16-row tiles, each tile's
 //                 super-block 2304 contiguous bytes; repacked once at load),
-//                 f32 as given [out, in]
+//                 Q8_0 in its TILED layout (16-row tiles x 256-element
+//                 groups of 4352 bytes), f32 as given [out, in]
 //   K/V pools     [slot][layer][kv_head][max_seq][head_dim] f32
 //   RoPE table    [max_seq][head_dim/2][2] f32 (host-computed angles)
 //   activations   [T][...] f32, packed token-major; split-K partials
@@ -31,17 +32,24 @@ using namespace slate_hip;
 namespace {
 
 constexpr int DT_F32 = 0;
+constexpr int DT_Q8_0 = 16;
 constexpr int DT_Q4K = 18;
 
 struct Lin {
-    void* w = nullptr;       // Q4_K: TILED layout
+    void* w = nullptr;       // Q4_K, Q8_0: TILED layouts
     int dtype = DT_F32;
     int M = 0, K = 0;
     // bytes of the tensor in slate's own layout (the algorithmic weight bytes)
     size_t bytes() const {
-        return dtype == DT_Q4K ? (size_t)M * (K / QK) * QBLOCK : (size_t)M * K * sizeof(float);
+        if (dtype == DT_Q4K) return (size_t)M * (K / QK) * QBLOCK;
+        if (dtype == DT_Q8_0) return (size_t)M * (K / Q8_ELEMS) * Q8_BYTES;
+        return (size_t)M * K * sizeof(float);
     }
-    size_t dev_bytes() const { return dtype == DT_Q4K ? q4k_tiled_bytes(M, K) : bytes(); }
+    size_t dev_bytes() const {
+        if (dtype == DT_Q4K) return q4k_tiled_bytes(M, K);
+        if (dtype == DT_Q8_0) return q8_tiled_bytes(M, K);
+        return bytes();
+    }
 };
 
 struct LayerDev {
@@ -73,6 +81,7 @@ struct slate_hip_llama {
     bool tokenwise_attn = false;   // prompt-chunk tokens through the decode attention kernel
     float *att_po = nullptr, *att_pml = nullptr;
     Act16 act{};
+    Act8 act8{};                   // allocated with the first Q8_0 linear
     int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
             *last_tok = nullptr, *status = nullptr, *next = nullptr;
     int64_t* kv_base = nullptr;
@@ -276,11 +285,23 @@ struct RowStage {
     }
 };
 
-// Repack a Q4_K tensor staged in row layout into l.w (TILED).
+// The Q8_0 activation operand for the widest matmul input, T_pad rows.
+int ensure_act8(slate_hip_llama* m) {
+    if (m->act8.frag) return 0;
+    const int Kmax = std::max(m->cfg.d_model, m->cfg.ffn_hidden);
+    char* fr = nullptr;
+    if (dalloc(m, &fr, act8_bytes(m->tpad_cap, Kmax))) return -2;
+    m->act8 = Act8{fr, 0, m->tpad_cap, Kmax};
+    return 0;
+}
+
+// Repack a Q4_K or Q8_0 tensor staged in row layout into l.w (TILED).
 int tile_lin(slate_hip_llama* m, Lin& l, const void* row_dev) {
     char* p;
+    if (l.dtype == DT_Q8_0 && ensure_act8(m)) return -2;
     if (dalloc(m, &p, l.dev_bytes())) return -2;
     l.w = p;
+    if (l.dtype == DT_Q8_0) return launch_q8_tile(p, row_dev, l.M, l.K, stream());
     return launch_q4k_tile(p, row_dev, l.M, l.K, stream());
 }
 
@@ -288,12 +309,18 @@ int set_lin(slate_hip_llama* m, Lin& l, const void* host, int dtype, int M, int 
     l.M = M;
     l.K = K;
     l.dtype = dtype;
-    if (dtype != DT_F32 && dtype != DT_Q4K) {
-        set_error(-5, "engine: weight dtype %d not supported (f32=0, q4_k=18)", dtype);
+    // the dispatch of llama_infer.c:43-51, with Q8_0 routed to its own
+    // matmul (the reference reads a dtype-16 tensor as f32)
+    if (dtype != DT_F32 && dtype != DT_Q4K && dtype != DT_Q8_0) {
+        set_error(-5, "engine: weight dtype %d not supported (f32=0, q8_0=16, q4_k=18)", dtype);
         return -5;
     }
     if (dtype == DT_Q4K && K % QK) {
         set_error(-1, "engine: Q4_K weight with K=%d (not a multiple of 256)", K);
+        return -1;
+    }
+    if (dtype == DT_Q8_0 && K % Q8_ELEMS) {
+        set_error(-1, "engine: Q8_0 weight with K=%d (not a multiple of 32)", K);
         return -1;
     }
     if (dtype == DT_F32) return upload(m, &l.w, host, l.bytes());
@@ -350,13 +377,16 @@ void prof_collect(slate_hip_llama* m) {
     m->prof_used = 0;
 }
 
-// What a matmul group reads: the Q4_K activation operand and/or f32 rows.
+// What a matmul group reads: the Q4_K activation operand and/or f32 rows
+// (f32 linears read them directly, Q8_0 linears through their own operand
+// built from them).
 struct GroupIn {
-    bool q4 = false, f32 = false;
+    bool q4 = false, q8 = false, f32 = false;
+    bool rows() const { return q8 || f32; }
 };
 GroupIn group_in(const Lin* const* lins, int nl) {
     GroupIn g;
-    for (int i = 0; i < nl; ++i) (lins[i]->dtype == DT_Q4K ? g.q4 : g.f32) = true;
+    for (int i = 0; i < nl; ++i) (lins[i]->dtype == DT_Q4K ? g.q4 : (lins[i]->dtype == DT_Q8_0 ? g.q8 : g.f32)) = true;
     return g;
 }
 
@@ -372,12 +402,13 @@ Act16 act_for(slate_hip_llama* m, int T, int K) {
 // RMSNorm whose row factor is applied by the consumer of the group's matmul
 // (residual_act + RowNorm): only for all-Q4_K groups of width % 256 == 0.
 bool defer_norm(const slate_hip_llama* m, const GroupIn& gi, int D) {
-    return m->defer_norm && gi.q4 && !gi.f32 && D % QK == 0;
+    return m->defer_norm && gi.q4 && !gi.rows() && D % QK == 0;
 }
 
 // One matmul group: the linears in `lins` read the same input (operand `a`
-// for Q4_K, rows X [T, K] for f32) and write column ranges of one partial
-// buffer [S][T_pad][ldo]; *S_out = S.
+// for Q4_K, rows X [T, K] for f32 and Q8_0) and write column ranges of one
+// partial buffer [S][T_pad][ldo]; *S_out = S.  Q8_0 linears write the split
+// count the Q4_K ones chose, f32 linears force one split.
 int mm_group(slate_hip_llama* m, const Act16* a, const float* X, int T, int K, const Lin* const* lins,
              const int64_t* col, int nl, int64_t ldo, int* S_out, hipStream_t s) {
     const GroupIn gi = group_in(lins, nl);
@@ -399,6 +430,22 @@ int mm_group(slate_hip_llama* m, const Act16* a, const float* X, int T, int K, c
         int rc = launch_q4k(t, nq, true, *a, m->part, ldo, ss, max_splits, &S, s, prof_ev(m, e0), prof_ev(m, e1));
         if (rc) return rc;
         if (m->prof_on) m->prof_recs.push_back({tpad == 16 ? 0 : 3, bytes, e0, e1});
+    }
+    if (gi.q8) {
+        Act8 a8 = m->act8;
+        a8.rows = T;
+        a8.rows_pad = tpad;
+        a8.K = K;
+        int rc = launch_act8_from_f32(a8, X, K, s);
+        if (rc) return rc;
+        Q4kTarget t[3];
+        int nq = 0;
+        for (int i = 0; i < nl; ++i)
+            if (lins[i]->dtype == DT_Q8_0) t[nq++] = Q4kTarget{lins[i]->w, lins[i]->M, col[i]};
+        int S8 = 1;
+        rc = launch_q8(t, nq, a8, m->part, ldo, ss, max_splits, gi.q4 ? S : 0, &S8, s);
+        if (rc) return rc;
+        S = S8;
     }
     for (int i = 0; i < nl; ++i) {
         const Lin& l = *lins[i];
@@ -429,6 +476,17 @@ int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
             m->prof_recs.push_back({a.rows_pad == 16 ? 0 : 3, (double)l.bytes() + 4.0 * n * (c.d_model + c.vocab), e0,
                                     e1});
         return rc;
+    }
+    if (l.dtype == DT_Q8_0) {
+        Act8 a8 = m->act8;
+        a8.rows = n;
+        a8.rows_pad = row_pad(n);
+        a8.K = c.d_model;
+        int rc = launch_act8_from_f32(a8, m->xlast, c.d_model, s);
+        if (rc) return rc;
+        Q4kTarget t{l.w, c.vocab, 0};
+        int S = 1;
+        return launch_q8(&t, 1, a8, m->logits, c.vocab, 0, 1, 0, &S, s);
     }
     return launch_mm_f32(m->logits, m->xlast, (const float*)l.w, n, c.vocab, c.d_model, c.vocab, s);
 }
@@ -467,7 +525,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                 rc = launch_residual_act(m->x, li ? m->part : nullptr, S_prev, (int64_t)tpad * D, Ld.attn_norm, T, D,
                                          a, m->ssq, s);
             } else {
-                rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, li ? m->part : nullptr, S_prev,
+                rc = launch_rmsnorm_act(gi.rows() ? m->xn : nullptr, m->x, li ? m->part : nullptr, S_prev,
                                         (int64_t)tpad * D, Ld.attn_norm, T, D, c.rms_eps, gi.q4 ? &a : nullptr, s);
             }
             if (rc) return rc;
@@ -506,7 +564,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                 rn.nblk = D / QK;
                 rc = launch_residual_act(m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm, T, D, a, m->ssq, s);
             } else {
-                rc = launch_rmsnorm_act(gi.f32 ? m->xn : nullptr, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm,
+                rc = launch_rmsnorm_act(gi.rows() ? m->xn : nullptr, m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm,
                                         T, D, c.rms_eps, gi.q4 ? &a : nullptr, s);
             }
             if (rc) return rc;
@@ -518,9 +576,9 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             const GroupIn gi = group_in(g, 1);
             Act16 a = act_for(m, T, H);
             if (H % QK == 0)
-                rc = launch_silu_act(gi.f32 ? m->h : nullptr, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H,
+                rc = launch_silu_act(gi.rows() ? m->h : nullptr, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H,
                                      2 * H, gi.q4 ? &a : nullptr, rn, s);
-            else   // no Q4_K operand exists for this width (and no deferred norm: gate/up are f32)
+            else   // no Q4_K operand exists for this width (and no deferred norm: gate/up are not Q4_K)
                 rc = launch_silu_mul(m->h, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H, 2 * H, 2 * H, s);
             if (rc) return rc;
             if ((rc = mm_group(m, &a, m->h, T, H, g, col, 1, D, &S, s))) return rc;
@@ -652,8 +710,8 @@ slate_hip_llama_t* slate_hip_llama_new(const slate_hip_llama_config_t* cfg, cons
 slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t* cfg, uint64_t seed, int quant,
                                                  int max_slots, int max_tokens) {
     if (!device_ok()) return nullptr;
-    if (quant != DT_F32 && quant != DT_Q4K) {
-        set_error(-1, "llama_new_synthetic: quant must be 0 (f32) or 18 (q4_k)");
+    if (quant != DT_F32 && quant != DT_Q4K && quant != DT_Q8_0) {
+        set_error(-1, "llama_new_synthetic: quant must be 0 (f32), 16 (q8_0) or 18 (q4_k)");
         return nullptr;
     }
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
@@ -669,8 +727,8 @@ slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t*
         l.M = M;
         l.K = K;
         l.dtype = quant;
-        if (quant == DT_Q4K && K % QK) {
-            set_error(-1, "llama_new_synthetic: K=%d not a multiple of 256", K);
+        if ((quant == DT_Q4K && K % QK) || (quant == DT_Q8_0 && K % Q8_ELEMS)) {
+            set_error(-1, "llama_new_synthetic: K=%d not a multiple of the block size", K);
             return -1;
         }
         uint64_t sd = mix(seed, ++tid);
@@ -687,7 +745,7 @@ slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t*
         }
         void* row = st.get(l.bytes());
         if (!row) return -2;
-        int rc = launch_synth_q4k(row, M, K, sd, std, s);
+        int rc = quant == DT_Q8_0 ? launch_synth_q8(row, M, K, sd, std, s) : launch_synth_q4k(row, M, K, sd, std, s);
         return rc ? rc : tile_lin(m, l, row);
     };
     auto gen_f32 = [&](float** dst, int64_t n, float sd_std, float fill) -> int {
@@ -742,7 +800,7 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
         src = m->out.w;
         bytes = m->out.bytes();
         dt = m->out.dtype;
-        if (dt == DT_Q4K) tiled = &m->out;
+        if (dt == DT_Q4K || dt == DT_Q8_0) tiled = &m->out;
     }
     else if (n.rfind("blk.", 0) == 0) {
         int li = atoi(n.c_str() + 4);
@@ -765,7 +823,7 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
             src = l->w;
             bytes = l->bytes();
             dt = l->dtype;
-            if (dt == DT_Q4K) tiled = l;
+            if (dt == DT_Q4K || dt == DT_Q8_0) tiled = l;
         }
     } else {
         return -1;
@@ -784,7 +842,8 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
             set_error(-7, "get_tensor copy failed");
             return -7;
         }
-        q4k_untile_host((uint8_t*)host_dst, t.data(), tiled->M, tiled->K);
+        if (tiled->dtype == DT_Q8_0) q8_untile_host((uint8_t*)host_dst, t.data(), tiled->M, tiled->K);
+        else q4k_untile_host((uint8_t*)host_dst, t.data(), tiled->M, tiled->K);
         return (int64_t)bytes;
     }
     if (hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost) != hipSuccess) {

@@ -11,13 +11,9 @@
 
 #include "launch.h"
 #include "act16.h"
+#include "mfma.h"
 
 namespace slate_hip {
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // IEEE half -> float by integer arithmetic (precision.c:10-29 semantics,
 // exact for every input incl. subnormals, independent of FP mode bits).
@@ -164,11 +160,6 @@ __device__ __forceinline__ void load_wtile_tiled(WTile& w, const uint8_t* tb, in
     w.qb = *(const uint4*)(tb + 1280 + 16 * lane);
 }
 
-// Hardware half -> float (v_cvt_f32_f16; exact, subnormals included).
-__device__ __forceinline__ float f16_to_f32_hw(uint32_t h) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-
 // Per-block constants of one weight tile for lane group g: the f16 fma
 // terms that turn nibbles into q * sc (low nibble: 1024+q -> (1024+q)*sc -
 // 1024*sc; high nibble: 1024+16q -> (1024+16q)*(sc/16) - 64*sc), the
@@ -268,22 +259,6 @@ __device__ __forceinline__ void load_act_units(ActOp& A, floatx4& rs, const uint
     A.ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
     const float4 rv = __builtin_bit_cast(float4, sa[1088 + (lane >> 4)]);
     rs = floatx4{rv.x, rv.y, rv.z, rv.w};
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt
-// 7 << 4 | lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
-#define SH_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
-
-// Direct global -> LDS copy of 16 bytes per lane: lane i's bytes land at LDS
-// byte address lds + 16 i (lds wave-uniform).  Issued from inline assembly
-// so the compiler does not treat every later LDS read as waiting on it (its
-// LDS-DMA tracking would stall the weight prefetch too); callers wait with
-// SH_WAIT_VMCNT and a barrier before reading the copied units.
-__device__ __forceinline__ void lds_copy16(const void* gsrc, uint32_t lds) {
-    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(gsrc), "{m0}"(lds) : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 
 // Decode kernel (one 16-row activation tile).  A workgroup of four waves

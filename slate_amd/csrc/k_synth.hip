@@ -4,7 +4,8 @@
 // (seed, index) -> two uniforms -> Box-Muller), so any element can be
 // recomputed independently.  Q4_K tensors are quantised per super-block by
 // one thread with the same scale/min search as slate_amd/synth.py
-// (per sub-block min/max, 6-bit codes against the block maxima).
+// (per sub-block min/max, 6-bit codes against the block maxima); Q8_0
+// tensors per 32-element block with d = max|w| / 127 (as synth.py).
 #include "launch.h"
 
 namespace slate_hip {
@@ -99,6 +100,40 @@ int launch_synth_q4k(void* dst, int64_t rows, int64_t cols, uint64_t seed, float
     int64_t nblk = rows * (cols / QK);
     hipLaunchKernelGGL(synth_q4k_kernel, dim3((unsigned)((nblk + 127) / 128)), dim3(128), 0, s,
                        (uint8_t*)dst, nblk, cols, splitmix64(seed), std);
+    SH_CHECK_LAUNCH();
+    return 0;
+}
+
+__global__ void synth_q8_kernel(uint8_t* __restrict__ dst, int64_t nblocks_total, uint64_t key, float std) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks_total) return;
+    const uint64_t i0 = (uint64_t)b * Q8_ELEMS;    // row-major: block b covers elements 32b..32b+31
+    float v[Q8_ELEMS], amax = 0.f;
+    for (int e = 0; e < Q8_ELEMS; ++e) {
+        v[e] = std * normal_at(key, i0 + e);
+        amax = fmaxf(amax, fabsf(v[e]));
+    }
+    const _Float16 d16 = (_Float16)(amax / 127.0f);
+    const float d = (float)d16;
+    uint8_t* o = dst + b * Q8_BYTES;
+    const uint16_t db = __builtin_bit_cast(uint16_t, d16);
+    o[0] = db & 0xff;
+    o[1] = db >> 8;
+    for (int e = 0; e < Q8_ELEMS; ++e) {
+        const float q = d > 0.f ? fminf(fmaxf(rintf(v[e] / d), -127.f), 127.f) : 0.f;
+        o[2 + e] = (uint8_t)(int8_t)q;
+    }
+}
+
+int launch_synth_q8(void* dst, int64_t rows, int64_t cols, uint64_t seed, float std, hipStream_t s) {
+    if (rows <= 0) return 0;
+    if (cols % Q8_ELEMS) {
+        set_error(-1, "synth_q8_0: cols %lld not a multiple of 32", (long long)cols);
+        return -1;
+    }
+    const int64_t nblk = rows * (cols / Q8_ELEMS);
+    hipLaunchKernelGGL(synth_q8_kernel, dim3((unsigned)((nblk + 127) / 128)), dim3(128), 0, s, (uint8_t*)dst,
+                       nblk, splitmix64(seed), std);
     SH_CHECK_LAUNCH();
     return 0;
 }

@@ -68,6 +68,7 @@ int launch_attention_step(float* out, const float* q, const float* K, const floa
 // k_synth.hip
 int launch_synth_f32(float* dst, int64_t n, uint64_t seed, float std, float fill, hipStream_t s);
 int launch_synth_q4k(void* dst, int64_t rows, int64_t cols, uint64_t seed, float std, hipStream_t s);
+int launch_synth_q8(void* dst, int64_t rows, int64_t cols, uint64_t seed, float std, hipStream_t s);
 
 // Host-side RoPE table exactly as llama_infer.c:77-92 computes the angles:
 // cs[(p*half + i)*2 + {0,1}] = {cosf, sinf}(p * powf(theta, -2i/hd)).

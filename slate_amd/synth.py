@@ -1,4 +1,4 @@
-"""Seeded synthetic LLaMA-shaped models and a host-side Q4_K quantizer.
+"""Seeded synthetic LLaMA-shaped models and host-side Q4_K / Q8_0 quantizers.
 
 The quantizer writes slate's Q4_K layout (src/util/quant.c:135-166): 144-byte
 super-blocks of [f16 d][f16 dmin][12-byte packed 6-bit scales/mins][128 bytes
@@ -6,7 +6,8 @@ of nibbles], where sub-block j takes qs[16j..16j+15] with the low nibble of
 byte i as element i and the high nibble as element i+16.  The scale/min
 search is this project's own (per sub-block min/max, then 6-bit codes against
 the block maxima); any valid encoding serves, since parity is checked on the
-bytes it produces.
+bytes it produces.  Q8_0 (quant.c:12-25) is 34-byte blocks of [f16 d][32 x
+int8 q] with w = d * q; the encoder takes d = max|w| / 127 per block.
 """
 from __future__ import annotations
 
@@ -14,10 +15,12 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from .gguf import GGML_F32, GGML_Q4_K, GGUFWriter, SLATE_F32, SLATE_Q4_K
+from .gguf import GGML_F32, GGML_Q4_K, GGML_Q8_0, GGUFWriter, SLATE_F32, SLATE_Q4_K, SLATE_Q8_0
 
 QK = 256
 BLOCK_BYTES = 144
+Q8_ELEMS = 32
+Q8_BYTES = 34
 
 
 def pack_scales(qsc: np.ndarray, qmn: np.ndarray) -> np.ndarray:
@@ -61,6 +64,30 @@ def quantize_q4k(w: np.ndarray) -> bytes:
     qs = (q[..., :16] | (q[..., 16:] << 4)).reshape(M, nb, 128)
     out[..., 16:] = qs
     return out.tobytes()
+
+
+def quantize_q8_0(w: np.ndarray) -> bytes:
+    """Quantize f32 [M, K] (K % 32 == 0) row-major to Q8_0 bytes."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M, K = w.shape
+    assert K % Q8_ELEMS == 0
+    x = w.reshape(M, K // Q8_ELEMS, Q8_ELEMS)
+    d16 = (np.abs(x).max(-1) / 127.0).astype(np.float16)
+    d = d16.astype(np.float32)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(d > 0, np.clip(np.rint(x / d), -127, 127), 0).astype(np.int8)
+    out = np.zeros((M, K // Q8_ELEMS, Q8_BYTES), np.uint8)
+    out[..., 0:2] = d16.view(np.uint8).reshape(M, K // Q8_ELEMS, 2)
+    out[..., 2:] = q.view(np.uint8)
+    return out.tobytes()
+
+
+def dequantize_q8_0(raw, M: int, K: int) -> np.ndarray:
+    """numpy dequant with quant.c:12-25's arithmetic (one exact f32 product)."""
+    b = np.frombuffer(bytes(raw), np.uint8).reshape(M, K // Q8_ELEMS, Q8_BYTES)
+    d = b[..., 0:2].copy().view(np.float16).astype(np.float32)
+    q = b[..., 2:].copy().view(np.int8).astype(np.float32)
+    return (d * q).reshape(M, K)
 
 
 def dequantize_q4k(raw, M: int, K: int) -> np.ndarray:
@@ -121,8 +148,8 @@ def make_llama(shape: LlamaShape, seed: int, quant: str = "f32", output_quant: s
                std: float = 0.02):
     """Return {name: (array_or_bytes, slate_dtype, (out, in) shape)} with
     weights ~ N(0, std) from ``numpy.random.default_rng(seed)`` and norms 1.0
-    (as slate's fixtures do).  ``quant`` applies to the seven block linears,
-    ``output_quant`` (default: same) to the LM head."""
+    (as slate's fixtures do).  ``quant`` ("f32", "q4k" or "q8_0") applies to
+    the seven block linears, ``output_quant`` (default: same) to the LM head."""
     rng = np.random.default_rng(seed)
     oq = quant if output_quant is None else output_quant
 
@@ -133,6 +160,8 @@ def make_llama(shape: LlamaShape, seed: int, quant: str = "f32", output_quant: s
         a = w(shp)
         if q == "q4k":
             return (np.frombuffer(quantize_q4k(a), np.uint8), SLATE_Q4_K, shp)
+        if q == "q8_0":
+            return (np.frombuffer(quantize_q8_0(a), np.uint8), SLATE_Q8_0, shp)
         return (a, SLATE_F32, shp)
 
     t = {}
@@ -160,5 +189,5 @@ def write_llama_gguf(path, shape: LlamaShape, tensors: dict):
     g.add_f32("llama.rope.freq_base", shape.theta)
     g.add_f32("llama.attention.layer_norm_rms_epsilon", shape.eps)
     for name, (arr, dt, shp) in tensors.items():
-        g.add_tensor(name, shp, GGML_Q4_K if dt == SLATE_Q4_K else GGML_F32, arr)
+        g.add_tensor(name, shp, {SLATE_Q4_K: GGML_Q4_K, SLATE_Q8_0: GGML_Q8_0}.get(dt, GGML_F32), arr)
     g.write(path)

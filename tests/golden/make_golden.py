@@ -178,6 +178,32 @@ def main():
     g.update(q4_digest=np.array(tensors_digest(t)), q4_stream=np.array(q4_stream, np.int32),
              q4_logits=np.stack(q4_logits))
 
+    # ---- Q8_0: dequant, dot and matvec (quant.c:12-25, 64-133) --------------
+    # own generator, so the vectors above stay what they were
+    rng8 = np.random.default_rng(20261202)
+    M8, K8 = 5, 1024
+    b8 = rng8.integers(0, 256, (M8 * K8 // 32, 34), dtype=np.uint8)
+    heads = [0x0000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0x2E66, 0x8001, 0xAE66, 0x1C00, 0x7BFF]
+    for i in range(b8.shape[0]):
+        b8[i, 0:2] = np.frombuffer(np.uint16(heads[i % len(heads)]).tobytes(), np.uint8)
+        if i % 6 == 0:
+            b8[i, 2:] = 0x80                   # every q = -128
+        if i % 9 == 0:
+            b8[i, 2:] = 0x7F
+    raw8 = np.ascontiguousarray(b8.reshape(-1))
+    deq8 = np.empty(M8 * K8, np.float32)
+    ref.lib.slate_dequant_q8_0(fp(deq8), bp(raw8), M8 * K8)
+    mv8 = b8.copy()
+    mv8[:, 1] &= 0x3B                          # finite results for the matvec
+    mv8_raw = np.ascontiguousarray(mv8.reshape(-1))
+    X8 = rng8.normal(0, 1, (3, K8)).astype(np.float32)
+    Y8 = np.empty((3, M8), np.float32)
+    for i in range(3):
+        y = np.empty(M8, np.float32)
+        ref.lib.slate_q8_0_matvec(fp(y), bp(mv8_raw), fp(np.ascontiguousarray(X8[i])), M8, K8)
+        Y8[i] = y
+    g.update(q8_raw=raw8, q8_deq=deq8, q8_mv_raw=mv8_raw, q8_x=X8, q8_y=Y8, q8_MK=np.array([M8, K8]))
+
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {os.path.getsize(OUT)} bytes, {len(g)} arrays")
 

@@ -337,3 +337,68 @@ def test_f16_kv_cache_tolerance_study(orc, monkeypatch):
         for s in sess:
             s.free()
         m.free()
+
+
+MIXQ = LlamaShape(n_layers=2, d_model=1024, n_heads=8, n_kv_heads=4, ffn=2048, vocab=300, max_seq=160)
+
+
+def replay_against_oracle(orc, shape, t, m, prompts, n_decode):
+    """Prompt step for every sequence, then ragged decode steps; each
+    sequence's logits against the oracle replaying the engine's tokens."""
+    sess = [m.session() for _ in prompts]
+    rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+    assert rc == 0
+    steps = [lg]
+    toks = np.asarray(nxt, np.int32)
+    for _ in range(n_decode):
+        rc, lg, nxt = m.step(sess, [1] * len(prompts), toks)
+        assert rc == 0
+        steps.append(lg)
+        toks = np.asarray(nxt, np.int32)
+    om = OracleModel(orc, shape, t)
+    for i, p in enumerate(prompts):
+        o = om.session()
+        rc, want = o.prefill(p)
+        assert rc == 0 and relerr(steps[0][i], want) < TOL
+        tok = int(np.argmax(steps[0][i]))
+        for k in range(1, len(steps)):
+            rc, want = o.decode(tok)
+            assert rc == 0 and relerr(steps[k][i], want) < TOL, (i, k)
+            tok = int(np.argmax(steps[k][i]))
+
+
+def test_q8_0_llama_matches_oracle(orc):
+    """All linears and the LM head Q8_0 (dtype 16, which the reference's
+    dispatch would read as f32): a 68-token prompt step (prefill kernels
+    over 8 activation tiles) and ragged decode steps against the oracle's
+    corrected dispatch; weights read back in slate's row layout unchanged."""
+    t = make_llama(FUSE, 77, quant="q8_0", output_quant="q8_0")
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, FUSE.vocab, n).astype(np.int32) for n in (40, 25, 3)]
+    m = slate_amd.Llama.from_tensors(FUSE, t, max_slots=4, max_tokens=96)
+    for name in ("blk.0.attn_q.weight", "blk.1.ffn_down.weight", "output.weight"):
+        raw, dt = m.get_tensor(name.rsplit(".", 1)[0])
+        assert dt == 16 and np.array_equal(raw, t[name][0])
+    replay_against_oracle(orc, FUSE, t, m, prompts, 6)
+
+
+def test_mixed_dtype_groups_match_oracle(orc):
+    """Q4_K, Q8_0 and f32 linears sharing one input: the QKV group mixes
+    Q4_K and Q8_0 (the Q8_0 kernel writes the split count the Q4_K launch
+    chose), gate/up mix Q8_0 and Q4_K, down is f32, o and the LM head Q8_0."""
+    from slate_amd.synth import quantize_q4k, quantize_q8_0
+    t = make_llama(MIXQ, 99, quant="f32", output_quant="f32")
+    kinds = {"attn_q": "q4k", "attn_k": "q8_0", "attn_v": "q4k", "attn_output": "q8_0",
+             "ffn_gate": "q8_0", "ffn_up": "q4k", "ffn_down": "f32"}
+    for name in list(t):
+        base = name.rsplit(".", 1)[0].split(".")[-1]
+        kind = "q8_0" if name == "output.weight" else kinds.get(base)
+        a, _, shp = t[name]
+        if kind == "q4k":
+            t[name] = (np.frombuffer(quantize_q4k(a), np.uint8), 18, shp)
+        elif kind == "q8_0":
+            t[name] = (np.frombuffer(quantize_q8_0(a), np.uint8), 16, shp)
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, MIXQ.vocab, n).astype(np.int32) for n in (9, 1, 30)]
+    m = slate_amd.Llama.from_tensors(MIXQ, t, max_slots=4, max_tokens=48)
+    replay_against_oracle(orc, MIXQ, t, m, prompts, 4)

@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 
 from oracle.pyoracle import OracleModel, bp, fp, ip
-from slate_amd.synth import dequantize_q4k, make_llama, pack_scales, quantize_q4k
+from slate_amd.synth import (dequantize_q4k, dequantize_q8_0, make_llama, pack_scales, quantize_q4k,
+                             quantize_q8_0)
 from tests.helpers import (N_GEN, N_SEQ, Q4, Q4_PROMPT, Q4_SEED, TINY, TINY_SEED, bits, relerr,
                            tensors_digest, tiny_prompts)
 
@@ -83,6 +84,89 @@ def test_q4k_matvec_vs_float64(orc):
     ref = x.astype(np.float64) @ deq.T
     assert np.max(np.abs(Y - ref) / (np.abs(ref) + 1e-9)) < 1e-4
     assert relerr(Y, ref) < 1e-6
+
+
+# ---------------------------------------------------------------------- Q8_0
+def test_q8_dequant_matches_golden(orc, golden):
+    raw = golden["q8_raw"]
+    got = orc.dequant_q8_0(raw, raw.size // 34 * 32)
+    assert np.array_equal(bits(got), bits(golden["q8_deq"]))
+    M, K = golden["q8_MK"]
+    assert np.array_equal(bits(dequantize_q8_0(raw, M, K).ravel()), bits(golden["q8_deq"]))
+
+
+def test_q8_dequant_known_answer(orc):
+    """slate's tests/test_quant.c:25-41: d = 0.1, q = i - 16 -> 0.1 * (i - 16)
+    within 0.01; and d * q is one exact f32 product (19 significant bits)."""
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.1).tobytes(), np.uint8)
+    blk[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    out = orc.dequant_q8_0(blk, 32)
+    assert np.all(np.abs(out - 0.1 * (np.arange(32) - 16)) <= 0.01)
+    exact = np.float64(np.float16(0.1)) * (np.arange(32) - 16)
+    assert np.array_equal(out.astype(np.float64), exact)
+
+
+def test_q8_matvec_matches_golden(orc, golden):
+    M, K = golden["q8_MK"]
+    Y = orc.q8_0_matmul(golden["q8_mv_raw"], golden["q8_x"], M, K)
+    assert np.array_equal(bits(Y), bits(golden["q8_y"]))
+
+
+def test_q8_matvec_vs_float64(orc):
+    """slate's tests/test_q8_dot.c method (K=256, M=8, uniform values in
+    [-1, 1]): the fast dot within rel 1e-4 of the dequantised float64 dot;
+    plus a large-K case."""
+    rng = np.random.default_rng(11)
+    for M, K in ((8, 256), (16, 4096)):
+        W = (rng.integers(-1000, 1001, (M, K)) / 1000.0).astype(np.float32)
+        raw = np.frombuffer(quantize_q8_0(W), np.uint8).copy()
+        x = (rng.integers(-1000, 1001, (2, K)) / 1000.0).astype(np.float32)
+        Y = orc.q8_0_matmul(raw, x, M, K)
+        deq = orc.dequant_q8_0(raw, M * K).reshape(M, K).astype(np.float64)
+        assert np.abs(deq - W).max() <= np.abs(W).max() / 127 * 0.51 + 1e-6   # half a step
+        ref = x.astype(np.float64) @ deq.T
+        assert np.max(np.abs(Y - ref) / (np.abs(ref) + 1e-6)) < 1e-4
+        assert relerr(Y, ref) < 1e-6
+
+
+def test_q8_dot_lane_order_is_pinned(orc):
+    """The eight-lane order is what makes the result bit-exact: a plain
+    sequential float sum of the same products differs on some rows."""
+    rng = np.random.default_rng(12)
+    M, K = 64, 1024
+    raw = rng.integers(0, 256, (M * K // 32, 34), dtype=np.uint8)
+    raw[:, 1] &= 0x3B
+    raw = np.ascontiguousarray(raw.reshape(-1))
+    x = rng.normal(0, 1, K).astype(np.float32)
+    Y = orc.q8_0_matmul(raw, x, M, K)[0]
+    deq = orc.dequant_q8_0(raw, M * K).reshape(M, K)
+    seq = np.zeros(M, np.float32)
+    for k in range(K):
+        seq = (seq + deq[:, k] * x[k]).astype(np.float32)
+    assert not np.array_equal(bits(Y), bits(seq))
+    ref = deq.astype(np.float64) @ x.astype(np.float64)
+    assert relerr(Y, ref) < 1e-5
+
+
+def test_q8_llama_equals_its_dequantised_f32_model(orc):
+    """The corrected dtype dispatch: a model whose linears are Q8_0 gives the
+    logits of the same model with those weights dequantised to f32 (the f32
+    path sums in another order, so within float rounding)."""
+    t = make_llama(Q4, Q4_SEED, quant="q8_0", output_quant="q8_0")
+    f = {}
+    for name, (a, dt, shp) in t.items():
+        f[name] = ((orc.dequant_q8_0(a, shp[0] * shp[1]).reshape(shp), 0, shp) if dt == 16 else (a, dt, shp))
+    s8, sf = OracleModel(orc, Q4, t).session(), OracleModel(orc, Q4, f).session()
+    rc8, l8 = s8.prefill(Q4_PROMPT)
+    rcf, lf = sf.prefill(Q4_PROMPT)
+    assert rc8 == rcf == 0
+    for k in range(6):
+        assert relerr(l8, lf) < 1e-5
+        tok = int(np.argmax(lf))
+        rc8, l8 = s8.decode(tok)
+        rcf, lf = sf.decode(tok)
+    assert relerr(l8, lf) < 1e-5
 
 
 # ------------------------------------------------------------ vtable KATs
@@ -323,6 +407,14 @@ def test_oracle_bitexact_with_live_reference(orc, ref):
     orc.lib.orc_rope_row(fp(r1), 8, 64, 4321, 500000.0)
     ref.lib.ref_rope_inplace_row(fp(r2), 8, 64, 4321, 500000.0)
     assert np.array_equal(bits(r1), bits(r2))
+    raw8 = np.frombuffer(quantize_q8_0(W), np.uint8).copy()
+    a = orc.dequant_q8_0(raw8, W.size)
+    ref.lib.slate_dequant_q8_0(fp(b), bp(raw8), W.size)
+    assert np.array_equal(bits(a), bits(b))
+    y1 = orc.q8_0_matmul(raw8, x, 32, 1024)[0]
+    y2 = np.empty(32, np.float32)
+    ref.lib.slate_q8_0_matvec(fp(y2), bp(raw8), fp(x), 32, 1024)
+    assert np.array_equal(bits(y1), bits(y2))
     h = np.arange(0, 31744, 7, dtype=np.uint16)      # finite positive halves
     assert all(np.float32(orc.lib.orc_f16_to_f32(int(v))).view(np.uint32) ==
                np.float32(ref.lib.slate_f16_to_f32(int(v))).view(np.uint32) for v in h)
