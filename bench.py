@@ -21,8 +21,8 @@ on the same weights and KV state, for one step of all 16 sequences.
 kernels.hbm_copy_GBs = a measured 1 GiB device copy (read + write bytes /
 time) beside the nominal 8 TB/s.
 
---ops instead prints the op-level figures (one JSON object): the Q4_K matmul
-through the C ABI at (M, K) in {(4096, 4096), (14336, 4096), (4096, 14336)}
+--ops instead prints the op-level figures (one JSON object): the Q4_K and
+Q8_0 matmuls through the C ABI (pre-tiled weights) at (M, K) in {(4096, 4096), (14336, 4096), (4096, 14336)}
 and B in {1, 4, 16, 64}, rotating over enough weight copies (> 300 MB) that
 the 256 MB Infinity Cache cannot hold them; and ragged GQA attention with
 B = 64 sequences, 32 q / 8 kv heads, head_dim 128, lengths
@@ -130,7 +130,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device-to-device copy 5 times and exit")
-    ap.add_argument("--ops", action="store_true", help="op-level Q4_K matmul and ragged attention figures")
+    ap.add_argument("--ops", action="store_true", help="op-level Q4_K / Q8_0 matmul and ragged attention figures")
     args = ap.parse_args()
     if args.copy_calibration:
         import torch
@@ -302,47 +302,55 @@ def graph_time_us(fn, calls, stream, result):
 
 
 def run_ops(seed):
-    """C2 (Q4_K matmul) and C3 (ragged attention) op figures."""
+    """C2 (Q4_K and Q8_0 matmuls at the 8B linear shapes) and C3 (ragged
+    attention) op figures."""
     import torch
     import slate_amd
     lib = slate_amd.load_library()
     slate_amd.Backend()
     stream = torch.cuda.ExternalStream(lib.slate_hip_stream())
     out = {"metric": "op-level device time per call", "hbm_peak_GBs": HBM_PEAK_GBS,
-           "mfma_f16_peak_TFLOPs": 2500.0, "hbm_copy_GBs": round(copy_bandwidth(), 1), "q4k": [],
+           "mfma_f16_peak_TFLOPs": 2500.0, "hbm_copy_GBs": round(copy_bandwidth(), 1), "q4k": [], "q8_0": [],
            "attention": None}
     gen = torch.Generator(device="cuda").manual_seed(seed)
-    for M, K in ((4096, 4096), (14336, 4096), (4096, 14336)):
-        nblk = M * K // 256
-        raw = torch.randint(0, 256, (nblk, 144), dtype=torch.uint8, device="cuda", generator=gen)
-        raw[:, 1] = (raw[:, 1] & 0x1F) | 0x10        # finite, moderate d and dmin
-        raw[:, 3] = (raw[:, 3] & 0x1F) | 0x10
-        tb = lib.slate_hip_q4k_tiled_bytes(M, K)
-        ncopy = max(32, -(-300_000_000 // tb) + 1)
-        copies = torch.empty((ncopy, tb), dtype=torch.uint8, device="cuda")
-        torch.cuda.synchronize()
-        for c in range(ncopy):
-            slate_amd.check(lib.slate_hip_q4k_tile(copies[c].data_ptr(), raw.data_ptr(), M, K), "q4k_tile")
-        lib.slate_hip_sync()
-        del raw
-        for B in (1, 4, 16, 64):
-            X = torch.randn(B, K, device="cuda", generator=gen)
-            Y = torch.empty(B, M, device="cuda")
+    # (block elements, block bytes, high byte of each f16 scale, tiler, tiled matmul)
+    formats = {"q4k": (256, 144, (1, 3), lib.slate_hip_q4k_tiled_bytes, lib.slate_hip_q4k_tile,
+                       lib.slate_hip_matmul_q4k_tiled),
+               "q8_0": (32, 34, (1,), lib.slate_hip_q8_0_tiled_bytes, lib.slate_hip_q8_0_tile,
+                        lib.slate_hip_matmul_q8_0_tiled)}
+    for fmt, (qk, qb, hi, tiled_bytes, tile, matmul) in formats.items():
+        for M, K in ((4096, 4096), (14336, 4096), (4096, 14336)):
+            nblk = M * K // qk
+            raw = torch.randint(0, 256, (nblk, qb), dtype=torch.uint8, device="cuda", generator=gen)
+            for b in hi:                                 # finite, moderate scales
+                raw[:, b] = (raw[:, b] & 0x1F) | 0x10
+            tb = tiled_bytes(M, K)
+            # rotate over > 300 MB of copies so every call streams from HBM
+            ncopy = max(32, -(-300_000_000 // tb) + 1)
+            copies = torch.empty((ncopy, tb), dtype=torch.uint8, device="cuda")
             torch.cuda.synchronize()
+            for c in range(ncopy):
+                slate_amd.check(tile(copies[c].data_ptr(), raw.data_ptr(), M, K), fmt + " tile")
+            lib.slate_hip_sync()
+            del raw
+            for B in (1, 4, 16, 64):
+                X = torch.randn(B, K, device="cuda", generator=gen)
+                Y = torch.empty(B, M, device="cuda")
+                torch.cuda.synchronize()
 
-            def call(i, X=X, Y=Y, B=B):
-                slate_amd.check(lib.slate_hip_matmul_q4k_tiled(Y.data_ptr(), copies[i % ncopy].data_ptr(),
-                                                               X.data_ptr(), B, M, K), "matmul_q4k_tiled")
-            us, same = graph_time_us(call, 2 * ncopy, stream, Y)
-            alg = M * K // 256 * 144 + 4 * B * K + 4 * B * M
-            flops = 2.0 * B * M * K
-            out["q4k"].append({"M": M, "K": K, "B": B, "us": round(us, 2),
-                               "GBs": round(alg / us / 1e3, 1), "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 3),
-                               "TFLOPs": round(flops / us / 1e6, 1),
-                               "frac_mfma": round(flops / us / 1e6 / 2500.0, 4), "replays_match_eager": same})
-            log(out["q4k"][-1])
-        del copies
-        torch.cuda.empty_cache()
+                def call(i, X=X, Y=Y, B=B):
+                    slate_amd.check(matmul(Y.data_ptr(), copies[i % ncopy].data_ptr(), X.data_ptr(), B, M, K),
+                                    fmt + " matmul")
+                us, same = graph_time_us(call, 2 * ncopy, stream, Y)
+                alg = nblk * qb + 4 * B * K + 4 * B * M
+                flops = 2.0 * B * M * K
+                out[fmt].append({"M": M, "K": K, "B": B, "us": round(us, 2),
+                                 "GBs": round(alg / us / 1e3, 1), "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 3),
+                                 "TFLOPs": round(flops / us / 1e6, 1),
+                                 "frac_mfma": round(flops / us / 1e6 / 2500.0, 4), "replays_match_eager": same})
+                log(fmt, out[fmt][-1])
+            del copies
+            torch.cuda.empty_cache()
     # C3: ragged attention
     rng = np.random.default_rng(seed)
     Bq, Hq, Hkv, hd = 64, 32, 8, 128

@@ -636,7 +636,7 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         const int slots = pf_slots(NT);
         int S = 1;
         double best = 1e30;
-        for (int c = 1; c <= 8 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
+        for (int c = 1; c <= 16 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
             const int rounds = (tasks * c + slots - 1) / slots;
             const double cost = (double)rounds / c;
             if (cost < best - 1e-9) { best = cost; S = c; }

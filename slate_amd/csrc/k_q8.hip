@@ -402,8 +402,8 @@ static Q4kTargets q8_targets(const Q4kTarget* t, int n, int R) {
 }
 
 // Plan: one activation tile -> four-wave workgroups and the largest R in
-// {4, 2, 1}, then the fewest splits, reaching `target` workgroups (about two
-// per CU); more tiles -> eight-wave workgroups of R = 2 over NT = 4 (or 2)
+// {2, 1} (R = 4 only when forced), then the fewest splits, reaching `target`
+// workgroups (about two per CU); more tiles -> eight-wave workgroups of R = 2 over NT = 4 (or 2)
 // activation tiles, splits as long as they fill the chip.  Splits keep >= 2
 // groups each unless forced.
 int launch_q8(const Q4kTarget* t, int n, const Act8& a, float* out, int64_t ldo, int64_t split_stride,
@@ -420,8 +420,10 @@ int launch_q8(const Q4kTarget* t, int n, const Act8& a, float* out, int64_t ldo,
     int s_cap = std::min(max_splits, std::max(1, ngrp / 2));
     int R = 2, S = 1;
     if (act_tiles == 1) {
+        // R = 2 before R = 1: measured ahead of R = 4 (more groups per split
+        // beat more tiles per wave at these sizes)
         bool done = false;
-        for (int r = 4; r >= 1 && !done; r >>= 1) {
+        for (int r = R_env == 4 ? 4 : 2; r >= 1 && !done; r >>= 1) {
             if ((R_env == 1 || R_env == 2 || R_env == 4) && r != R_env) continue;
             int groups = 0;
             for (int i = 0; i < n; ++i) groups += ((t[i].M + 15) / 16 + r - 1) / r;
@@ -439,7 +441,7 @@ int launch_q8(const Q4kTarget* t, int n, const Act8& a, float* out, int64_t ldo,
         const int per_cu = (160 * 1024) / (2 * NT * ACT8_UNITS * 16);
         const int slots = cu_count() * std::max(1, per_cu);
         double best = 1e30;
-        for (int c = 1; c <= 8 && c <= s_cap; c *= 2) {
+        for (int c = 1; c <= 16 && c <= s_cap; c *= 2) {
             const double cost = (double)((tasks * c + slots - 1) / slots) / c;
             if (cost < best - 1e-9) { best = cost; S = c; }
         }
