@@ -540,11 +540,24 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
         const int L = tok_pos[t] + 1;
         const int nch = min((L + ATT_CHUNK - 1) / ATT_CHUNK, nch_max);
         const size_t p0 = ((size_t)t * Hq + hq) * nch_max;
-        // partials are loaded eight chunks at a time (clamped to the last
-        // chunk, used under a predicate) and combined in chunk order
+        // the first eight chunks' (max, sum) and outputs are loaded in one
+        // batch (clamped to the last chunk, used under a predicate): one
+        // round trip for contexts up to eight chunks; the max over every
+        // chunk is taken before any chunk is accumulated, in chunk order
         constexpr int MB = 8;
+        float2 ml[MB];
+        float4 ov[MB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const size_t pc = p0 + min(i, max(nch - 1, 0));
+            ml[i] = *(const float2*)(pml + pc * 2);
+            ov[i] = *(const float4*)(po + pc * HD + d);
+        }
         float M = -INFINITY;
-        for (int c0 = 0; c0 < nch; c0 += MB) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            if (i < nch) M = fmaxf(M, ml[i].x);
+        for (int c0 = MB; c0 < nch; c0 += MB) {
             float mv[MB];
 #pragma unroll
             for (int i = 0; i < MB; ++i) mv[i] = pml[(p0 + min(c0 + i, nch - 1)) * 2];
@@ -554,9 +567,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
         }
         float den = 0.f;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int c0 = 0; c0 < nch; c0 += MB) {
-            float2 ml[MB];
-            float4 ov[MB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            if (i < nch) {
+                const float f = expf(ml[i].x - M);
+                den += f * ml[i].y;
+                acc.x += f * ov[i].x; acc.y += f * ov[i].y; acc.z += f * ov[i].z; acc.w += f * ov[i].w;
+            }
+        for (int c0 = MB; c0 < nch; c0 += MB) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
                 const size_t pc = p0 + min(c0 + i, nch - 1);

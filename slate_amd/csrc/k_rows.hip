@@ -175,6 +175,7 @@ int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int 
 // operand.  The consumer of the matmul that follows multiplies each row by
 // row_inv_rms() (the matmul is linear in each row), so no kernel has to wait
 // for a whole row.  Rows >= rows write zero operand rows.
+template <bool DELTA>
 __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x, const float* __restrict__ delta,
                                                            int nsplit, int64_t split_stride,
                                                            const float* __restrict__ w, int rows, int D, Act16 a,
@@ -188,12 +189,17 @@ __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x
     const int e = kb * QK + 4 * lane;
     float4 yv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < rows) {
+        // x, w and the first eight partials are issued together: one
+        // memory round trip before any arithmetic
         float* xr = x + (size_t)r * D + e;
+        const float* dp = DELTA ? delta + (size_t)r * D + e : nullptr;
         float4 xv = *(const float4*)xr;
-        if (delta) {
-            const float4 sm = split_sum4(delta + (size_t)r * D + e, nsplit, split_stride);
+        const float4 wv = *(const float4*)(w + e);
+        Split4 pre;
+        if constexpr (DELTA) pre = split_load4(dp, nsplit, split_stride);
+        if constexpr (DELTA) {
+            const float4 sm = split_fin4(pre, dp, nsplit, split_stride);
             xv.x += sm.x; xv.y += sm.y; xv.z += sm.z; xv.w += sm.w;
-            *(float4*)xr = xv;
         }
         float sq = 0.f;
         sq = __builtin_fmaf(xv.x, xv.x, sq);
@@ -201,9 +207,9 @@ __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x
         sq = __builtin_fmaf(xv.z, xv.z, sq);
         sq = __builtin_fmaf(xv.w, xv.w, sq);
         sq = wave_sum(sq);
-        if (lane == 0) ssq[(size_t)r * nblk + kb] = sq;
-        const float4 wv = *(const float4*)(w + e);
         yv = make_float4(xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w);
+        if constexpr (DELTA) *(float4*)xr = xv;
+        if (lane == 0) ssq[(size_t)r * nblk + kb] = sq;
     }
     act16_store_block(a, r, kb, lane, yv);
 }
@@ -216,8 +222,13 @@ int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_
         return -1;
     }
     const int nblk = D / QK;
-    hipLaunchKernelGGL(residual_act_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, x, delta, nsplit,
-                       split_stride, w, rows, D, a, ssq);
+    const dim3 grid((nblk + 3) / 4, a.rows_pad);
+    if (delta && nsplit > 0)
+        hipLaunchKernelGGL(residual_act_kernel<true>, grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w, rows,
+                           D, a, ssq);
+    else
+        hipLaunchKernelGGL(residual_act_kernel<false>, grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w,
+                           rows, D, a, ssq);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -316,9 +327,13 @@ __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, co
     if (r < rows) {
         const float* gp = gate + (size_t)r * ld + e;
         const float* upp = up + (size_t)r * ld + e;
-        float4 g = split_sum4(gp, nsplit, split_stride), u = split_sum4(upp, nsplit, split_stride);
+        // gate, up and the row's block sums of squares in one round trip
+        const Split4 pg = split_load4(gp, nsplit, split_stride), pu = split_load4(upp, nsplit, split_stride);
+        RmsPre rp;
+        if (rn.ssq) rp = row_rms_load(rn.ssq, r, rn.nblk);
+        float4 g = split_fin4(pg, gp, nsplit, split_stride), u = split_fin4(pu, upp, nsplit, split_stride);
         if (rn.ssq) {   // gate and up are linear in the normalised row
-            const float inv = row_inv_rms(rn.ssq, r, rn.nblk, rn.D, rn.eps);
+            const float inv = row_rms_fin(rp, rn.ssq, r, rn.nblk, rn.D, rn.eps);
             g = make_float4(g.x * inv, g.y * inv, g.z * inv, g.w * inv);
             u = make_float4(u.x * inv, u.y * inv, u.z * inv, u.w * inv);
         }
@@ -363,33 +378,46 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, K
     const int ap = p < 0 ? -p : p;
     const float sg = p < 0 ? -1.0f : 1.0f;
     const float* pr = part + (size_t)t * qkv_ld;
-    // q, k, v are linear in the normalised row: apply its RMSNorm factor here
-    const float inv = rn.ssq ? row_inv_rms(rn.ssq, t, rn.nblk, rn.D, rn.eps) : 1.0f;
-    auto col = [&](int c) {
-        const float v = split_sum1(pr + c, nsplit, split_stride);
-        return rn.ssq ? v * inv : v;
-    };
+    // q, k, v are linear in the normalised row: its RMSNorm factor is
+    // applied here.  Every load that does not depend on the position (the
+    // partials of the lane's columns, the row's block sums) is issued before
+    // the position-dependent ones (rotation table, KV row).
+    RmsPre rp;
+    if (rn.ssq) rp = row_rms_load(rn.ssq, t, rn.nblk);
+    float inv = 1.0f;
+    auto scale = [&](float v) { return rn.ssq ? v * inv : v; };
     if (u < n_heads) {
         for (int i = lane; i < half; i += 64) {
             const int c0 = u * hd + i;
-            const float a = col(c0), b = col(c0 + half);
+            const Split1 pa = split_load1(pr + c0, nsplit, split_stride);
+            const Split1 pb = split_load1(pr + c0 + half, nsplit, split_stride);
             const float c = cs[((size_t)ap * half + i) * 2 + 0];
             const float sn = sg * cs[((size_t)ap * half + i) * 2 + 1];
+            if (rn.ssq) inv = row_rms_fin(rp, rn.ssq, t, rn.nblk, rn.D, rn.eps);
+            const float a = scale(split_fin1(pa, pr + c0, nsplit, split_stride));
+            const float b = scale(split_fin1(pb, pr + c0 + half, nsplit, split_stride));
             qout[(size_t)t * D + c0] = a * c - b * sn;
             qout[(size_t)t * D + c0 + half] = a * sn + b * c;
         }
     } else {
         const int kh = u - n_heads;
-        const int64_t base = kv_base[tok2seq[t]] + (int64_t)kh * head_stride + (int64_t)p * hd;
+        const int seq = tok2seq[t];
         for (int i = lane; i < half; i += 64) {
             const int ck = D + kh * hd + i, cv = D + kvd + kh * hd + i;
-            const float a = col(ck), b = col(ck + half);
+            const Split1 pa = split_load1(pr + ck, nsplit, split_stride);
+            const Split1 pb = split_load1(pr + ck + half, nsplit, split_stride);
+            const Split1 pv0 = split_load1(pr + cv, nsplit, split_stride);
+            const Split1 pv1 = split_load1(pr + cv + half, nsplit, split_stride);
             const float c = cs[((size_t)ap * half + i) * 2 + 0];
             const float sn = sg * cs[((size_t)ap * half + i) * 2 + 1];
+            const int64_t base = kv_base[seq] + (int64_t)kh * head_stride + (int64_t)p * hd;
+            if (rn.ssq) inv = row_rms_fin(rp, rn.ssq, t, rn.nblk, rn.D, rn.eps);
+            const float a = scale(split_fin1(pa, pr + ck, nsplit, split_stride));
+            const float b = scale(split_fin1(pb, pr + ck + half, nsplit, split_stride));
             Kpool[base + i] = (KVT)(a * c - b * sn);
             Kpool[base + i + half] = (KVT)(a * sn + b * c);
-            Vpool[base + i] = (KVT)col(cv);
-            Vpool[base + i + half] = (KVT)col(cv + half);
+            Vpool[base + i] = (KVT)scale(split_fin1(pv0, pr + cv, nsplit, split_stride));
+            Vpool[base + i + half] = (KVT)scale(split_fin1(pv1, pr + cv + half, nsplit, split_stride));
         }
     }
 }
