@@ -279,7 +279,9 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
     const int lane = tid & 63;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int wv = tid >> 6;
+    // wave-uniform (SGPR): the tensor selection and every weight and operand
+    // base address below are scalar; loads add the lane's offset
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = blockIdx.x * 4 + wv;
     const int ti = (tg.n > 2 && grp >= tg.grp0[2]) ? 2 : ((tg.n > 1 && grp >= tg.grp0[1]) ? 1 : 0);
     const uint8_t* W = ti == 2 ? tg.w[2] : (ti == 1 ? tg.w[1] : tg.w[0]);
@@ -303,10 +305,14 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
         else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
     };
     // copy block kb's units (kb < nblk: inside the operand buffer) into dst
+    const uint32_t o_act = 16 * lane;
     auto stage = [&](uint4* dst, int kb) {
-        for (int c = wv; c < CHUNKS; c += 4)
-            lds_copy16(frag + (size_t)kb * ACT_FRAG_UNITS + c * 64 + lane,
-                       __builtin_amdgcn_readfirstlane(lds_addr(dst + c * 64)));
+        const uint4* src = frag + (size_t)kb * ACT_FRAG_UNITS;
+#pragma unroll
+        for (int i = 0; i < (CHUNKS + 3) / 4; ++i) {
+            const int c = wv + 4 * i;
+            if (c < CHUNKS) lds_copy16(src + c * 64, o_act, lds_addr(dst + c * 64));
+        }
     };
     WTile w0[R], w1[R];
     floatx4 acc[R];
@@ -324,11 +330,12 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
     // sets swap roles each step (the loop is unrolled by two)
     auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
         const uint4* cur = s_act + (b & 1) * ACT_FRAG_UNITS;
-        const int kn = kb0 + min(b + 1, nb - 1);
-        if (b + 1 < nb) stage(s_act + ((b + 1) & 1) * ACT_FRAG_UNITS, kn);
-        __builtin_amdgcn_sched_barrier(0);
+        if (b + 1 < nb) {                               // the last block prefetches nothing
+            stage(s_act + ((b + 1) & 1) * ACT_FRAG_UNITS, kb0 + b + 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);   // unconditional (clamped) prefetch
+            for (int r = 0; r < R; ++r) ldw(wn[r], r, kb0 + b + 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (active) {
             // one K step at a time: the step's activation fragment is read
@@ -408,7 +415,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     const int lane = tid & 63;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int wv = tid >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // SGPR: scalar staging addresses
     // workgroup x -> tensor (tensors start on workgroup boundaries)
     const int wg = blockIdx.x;
     const int ti = (tg.n > 2 && wg >= tg.grp0[2]) ? 2 : ((tg.n > 1 && wg >= tg.grp0[1]) ? 1 : 0);
@@ -434,13 +441,16 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     };
     // copy block kb of activation tiles at0 .. at0+NT-1 (clamped) into `dst`
     // (every address stays inside the operand buffer: at < act_tiles, kb < nblk)
+    const uint32_t o_act = 16 * lane;
     auto stage = [&](uint4* dst, int kb) {
-        for (int c = wv; c < CHUNKS; c += WAVES) {
+#pragma unroll
+        for (int i = 0; i < (CHUNKS + WAVES - 1) / WAVES; ++i) {
+            const int c = wv + WAVES * i;
+            if (c >= CHUNKS) break;
             const int n = c / (ACT_FRAG_UNITS / 64);
             const int u = (c - n * (ACT_FRAG_UNITS / 64)) * 64;
             const int at = min(at0 + n, act_tiles - 1);
-            const uint4* src = frag + ((size_t)at * nblk + kb) * ACT_FRAG_UNITS + u + lane;
-            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + n * ACT_FRAG_UNITS + u)));
+            lds_copy16(frag + ((size_t)at * nblk + kb) * ACT_FRAG_UNITS + u, o_act, lds_addr(dst + n * ACT_FRAG_UNITS + u));
         }
     };
     WTile wc[R], wn[R];

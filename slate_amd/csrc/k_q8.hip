@@ -226,7 +226,7 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mm_kernel(Q4kTargets tg, const 
     const int lane = tid & 63;
     const int j = lane & 15;
     const int g = lane >> 4;
-    const int wv = tid >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // SGPR: scalar tensor and address math
     const int grp = blockIdx.x * WAVES + wv;
     const int ti = (tg.n > 2 && grp >= tg.grp0[2]) ? 2 : ((tg.n > 1 && grp >= tg.grp0[1]) ? 1 : 0);
     const uint8_t* W = ti == 2 ? tg.w[2] : (ti == 1 ? tg.w[1] : tg.w[0]);
@@ -262,11 +262,11 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mm_kernel(Q4kTargets tg, const 
     for (int r = 0; r < R; ++r) wp[r] = W + (size_t)min(tile0 + r, tiles - 1) * ngrp * Q8_TB;
     auto ldw = [&](Q8W& w, int r, int kb) { load_q8w(w, wp[r] + (size_t)kb * Q8_TB, lane); };
     // copy group kb's units of the nt tiles (kb < ngrp: inside the buffer)
+    const uint32_t o_act = 16 * lane;
     auto stage = [&](uint4* dst, int kb) {
         for (int c = wv; c < nt * TCH; c += WAVES) {
             const int n = c / TCH, u = (c - n * TCH) * 64;
-            lds_copy16(act + ((size_t)(at0 + n) * ngrp + kb) * ACT8_UNITS + u + lane,
-                       __builtin_amdgcn_readfirstlane(lds_addr(dst + n * ACT8_UNITS + u)));
+            lds_copy16(act + ((size_t)(at0 + n) * ngrp + kb) * ACT8_UNITS + u, o_act, lds_addr(dst + n * ACT8_UNITS + u));
         }
     };
     Q8W w0[R], w1[R];
