@@ -505,7 +505,8 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if (rc) return rc;
     if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
     // the decode attention work units depend only on positions: once per step
-    if ((rc = launch_attention_pairs(d_blk, m->n_dec, m->tok_pos, T, c.n_heads, c.max_seq, m->att_pml, s))) return rc;
+    if ((rc = launch_attention_pairs(d_blk, m->n_dec, m->tok_pos, m->tok2seq, m->kv_base, T, c.n_heads, c.max_seq,
+                                      m->att_pml, s))) return rc;
     const int tpad = row_pad(T);
     int S_prev = 0;
     RowNorm rn{};

@@ -173,25 +173,34 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_block_kernel(
 }
 
 // The (decode token, key chunk) work units that hold keys, in token order:
-// pairs[0] = count, pairs[1 + u] = i * 65536 + c for token list entry i
-// (dec_t0[i], or i) and chunk c < ceil((pos + 1) / ATT_CHUNK).  One
+// Decode work-unit list, built once per step: pairs[0] = count, then from
+// pairs + 4 (16-byte aligned) one int4 per unit {t * 65536 + c, pos,
+// kv_base low, kv_base high} for token list entry i (token t = dec_t0[i], or
+// i) and key chunk c < ceil((pos + 1) / ATT_CHUNK).  A unit's kernel thus
+// reads everything it needs before its first K load in one round trip.  One
 // workgroup; a block-wide scan per 1024 tokens.  Decode kernels launch
 // n_dec * nch_max units along x and take unit u from this list, so every
 // unit that streams keys is dispatched before the empty ones.
 __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restrict__ dec_t0, int n_dec,
-                                                          const int32_t* __restrict__ tok_pos, int nch_max,
+                                                          const int32_t* __restrict__ tok_pos,
+                                                          const int32_t* __restrict__ tok2seq,
+                                                          const int64_t* __restrict__ kv_base, int nch_max,
                                                           int32_t* __restrict__ pairs) {
     __shared__ int s_scan[1024];
     __shared__ int s_base;
     const int tid = threadIdx.x;
+    int4* units = (int4*)(pairs + 4);
     if (tid == 0) s_base = 0;
     __syncthreads();
     for (int i0 = 0; i0 < n_dec; i0 += 1024) {
         const int i = i0 + tid;
-        int n = 0;
+        int n = 0, t = 0, p = 0;
+        int64_t kvb = 0;
         if (i < n_dec) {
-            const int t = dec_t0 ? dec_t0[i] : i;
-            n = min((tok_pos[t] + ATT_CHUNK) / ATT_CHUNK, nch_max);
+            t = dec_t0 ? dec_t0[i] : i;
+            p = tok_pos[t];
+            kvb = kv_base[tok2seq[t]];
+            n = min((p + ATT_CHUNK) / ATT_CHUNK, nch_max);
         }
         s_scan[tid] = n;
         __syncthreads();
@@ -202,12 +211,35 @@ __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restr
             __syncthreads();
         }
         const int base = s_base + s_scan[tid] - n;
-        for (int c = 0; c < n; ++c) pairs[1 + base + c] = i * 65536 + c;
+        for (int c = 0; c < n; ++c)
+            units[base + c] = make_int4(t * 65536 + c, p, (int)(uint32_t)((uint64_t)kvb & 0xffffffffu),
+                                        (int)(uint32_t)((uint64_t)kvb >> 32));
         __syncthreads();
         if (tid == 1023) s_base += s_scan[1023];
         __syncthreads();
     }
     if (tid == 0) pairs[0] = s_base;
+}
+
+// Unit u of the list (both loads issued before either is used; u may lie
+// past the count, inside the list's storage, for the grid's empty tail).
+struct AttnUnit { int n, t, c, p; int64_t kvb; };
+__device__ __forceinline__ AttnUnit attn_unit(const int32_t* pairs, int u) {
+    const int n = pairs[0];
+    const int4 d = ((const int4*)(pairs + 4))[u];
+    AttnUnit r;
+    r.n = n;
+    r.t = d.x >> 16;
+    r.c = d.x & 0xffff;
+    r.p = d.y;
+    r.kvb = (int64_t)(((uint64_t)(uint32_t)d.w << 32) | (uint64_t)(uint32_t)d.z);
+    return r;
+}
+
+// Work-unit list storage inside the pml buffer (16-byte aligned).
+__host__ __device__ inline int32_t* attn_unit_list(float* pml, int T, int Hq, int nch_max) {
+    const uintptr_t a = (uintptr_t)(pml + (size_t)T * Hq * nch_max * 2);
+    return (int32_t*)((a + 15) & ~(uintptr_t)15);
 }
 
 // Four consecutive K/V elements as floats: f32 caches load 16 bytes, f16
@@ -244,11 +276,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     __shared__ float4 sred[4][G][LPR];
     // work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
     // wrote; the units past its count are the grid's empty tail
-    if ((int)blockIdx.x >= pairs[0]) return;
-    const int pr = pairs[1 + blockIdx.x];
-    const int c = pr & 0xffff, h = blockIdx.z;
-    const int t = dec_t0 ? dec_t0[pr >> 16] : (pr >> 16);
-    const int p = tok_pos[t];
+    const AttnUnit un = attn_unit(pairs, blockIdx.x);
+    if ((int)blockIdx.x >= un.n) return;
+    const int c = un.c, h = blockIdx.z, t = un.t, p = un.p;
     const int k0 = c * ATT_CHUNK;
     if (k0 > p) return;                            // merge never reads chunks past a token's end
     const int nk = min(p + 1 - k0, ATT_CHUNK);
@@ -256,7 +286,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int lg = lane >> 3, ls = lane & 7;
     const float scale = 1.0f / sqrtf((float)HD);
-    const int64_t base = kv_base[tok2seq[t]] + (int64_t)h * head_stride + (int64_t)k0 * HD;
+    const int64_t base = un.kvb + (int64_t)h * head_stride + (int64_t)k0 * HD;
     const KVT* Kh = Kp + base;
     const KVT* Vh = Vp + base;
     const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
@@ -377,18 +407,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
     __shared__ float s_m[4][G], s_l[4][G];
     // work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
     // wrote; the units past its count are the grid's empty tail
-    if ((int)blockIdx.x >= pairs[0]) return;
-    const int pr = pairs[1 + blockIdx.x];
-    const int c = pr & 0xffff, h = blockIdx.z;
-    const int t = dec_t0 ? dec_t0[pr >> 16] : (pr >> 16);
-    const int p = tok_pos[t];
+    const AttnUnit un = attn_unit(pairs, blockIdx.x);
+    if ((int)blockIdx.x >= un.n) return;
+    const int c = un.c, h = blockIdx.z, t = un.t, p = un.p;
     const int k0 = c * ATT_CHUNK;
     if (k0 > p) return;                            // merge never reads chunks past a token's end
     const int nk = min(p + 1 - k0, ATT_CHUNK);
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int lg = lane >> 3, ls = lane & 7;
     const float scale = 1.0f / sqrtf((float)HD);
-    const int64_t base = kv_base[tok2seq[t]] + (int64_t)h * head_stride + (int64_t)k0 * HD;
+    const int64_t base = un.kvb + (int64_t)h * head_stride + (int64_t)k0 * HD;
     const KVT* Kh = Kp + base;
     const KVT* Vh = Vp + base;
     const int kw0 = wv * KW;
@@ -643,7 +671,7 @@ int attn_prefill_block(int G) { return G > 0 && G <= 32 ? 32 / G : 1; }
 // work-unit list (1 + T * nch int32).
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos) {
     int nch = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
-    return (size_t)T * Hq * nch * (HD + 2) + (size_t)T * nch + 1;
+    return (size_t)T * Hq * nch * (HD + 2) + 4 * (size_t)T * nch + 12;   // + list header, units, alignment
 }
 
 // SLATE_HIP_ATTN_WAVE=0 selects the workgroup-phased decode kernel for every shape.
@@ -716,7 +744,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
         set_error(-5, "attention: %d query tokens / %d key chunks exceed the work-unit encoding", n_dec, nch_max);
         return -5;
     }
-    int32_t* pairs = (int32_t*)(pml + (size_t)T * Hq * nch_max * 2);
+    int32_t* pairs = attn_unit_list(pml, T, Hq, nch_max);
     AttnArgs a{q, Kp, Vp, nullptr, nullptr, tok2seq, tok_pos, kv_base, Hq, head_stride, nch_max, po, pml, ev_start,
                pairs, n_dec, kv_f16};
     for (int pass = 0; pass < 2; ++pass) {
@@ -730,7 +758,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
         if (!prefill && (HD == 32 || HD == 64 || HD == 128)) {
             if (!pairs_ready) {
                 SH_LAUNCH(a.ev0, nullptr, attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos,
-                          nch_max, pairs);
+                          tok2seq, kv_base, nch_max, pairs);
                 SH_CHECK_LAUNCH();
                 a.ev0 = nullptr;
             }
@@ -771,16 +799,16 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
                                    false);
 }
 
-int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, int T, int Hq, int max_pos,
-                           float* pml, hipStream_t s) {
+int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, const int32_t* tok2seq,
+                           const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s) {
     const int nch_max = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
     if (n_dec <= 0) return 0;
     if (n_dec >= 32768 || nch_max > 65536) {
         set_error(-5, "attention: %d query tokens / %d key chunks exceed the work-unit encoding", n_dec, nch_max);
         return -5;
     }
-    hipLaunchKernelGGL(attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, nch_max,
-                       (int32_t*)(pml + (size_t)T * Hq * nch_max * 2));
+    hipLaunchKernelGGL(attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, tok2seq, kv_base,
+                       nch_max, attn_unit_list(pml, T, Hq, nch_max));
     SH_CHECK_LAUNCH();
     return 0;
 }

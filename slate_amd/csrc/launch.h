@@ -55,8 +55,8 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
 // The decode work-unit list that launch_attention_blocks builds (in the tail
 // of the pml buffer) when pairs_ready is false: build it once when several
 // launches share the same tokens and positions (the layers of one step).
-int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, int T, int Hq, int max_pos,
-                           float* pml, hipStream_t s);
+int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, const int32_t* tok2seq,
+                           const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s);
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
 int launch_attention_ragged(float* out, const float* q, const float* Kp, const float* Vp,
                             const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,
