@@ -7,7 +7,12 @@
 // MFMA lanes read them (lane = 16 * g + j: row j of the tile, lane group g):
 //   unit (2t + h) * 64 + lane : x*s hi (h = 0) / lo (h = 1), elements
 //                               64g + 8t .. +7 of the block
-//   unit 1024 + lane          : (hi, lo) sums of sub-blocks 4*(g&1) .. +3
+//   unit 1024 + lane          : bytes 0..7, four halves: for g < 2 the hi
+//                               parts of the sums of sub-blocks 4g .. 4g+3,
+//                               for g >= 2 the lo parts of sub-blocks
+//                               4(g-2) .. +3 (the A operand of the one
+//                               16x16x16 MFMA of the min term); bytes 8..15
+//                               unused
 //   units 1088 .. 1091        : 1/s of rows 0..15 (f32); 1092.. padding
 // Each 256-element block of a row has its own exact power-of-two scale s with
 // max|x| * s in [2^14, 2^15); x*s = hi + lo; sub-block sums of x*s are stored
@@ -51,12 +56,11 @@ __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb,
     *(act_half4_t*)(fb + ((2 * t) * 64 + 16 * g + rr) * 16 + half_off) = h;
     *(act_half4_t*)(fb + ((2 * t + 1) * 64 + 16 * g + rr) * 16 + half_off) = l;
     if ((lane & 7) == 0) {
-        // sub-block s sits in the units of lane groups s>>2 and (s>>2) + 2
+        // sub-block s: hi half in lane group s>>2, lo half in lane group
+        // (s>>2) + 2, both as element s&3 of the unit
         const int g0 = sub >> 2;
-        const uint32_t pair = (uint32_t)__builtin_bit_cast(uint16_t, sh) |
-                              ((uint32_t)__builtin_bit_cast(uint16_t, sl) << 16);
-        *(uint32_t*)(fb + (1024 + 16 * g0 + rr) * 16 + 4 * (sub & 3)) = pair;
-        *(uint32_t*)(fb + (1024 + 16 * (g0 + 2) + rr) * 16 + 4 * (sub & 3)) = pair;
+        *(_Float16*)(fb + (1024 + 16 * g0 + rr) * 16 + 2 * (sub & 3)) = sh;
+        *(_Float16*)(fb + (1024 + 16 * (g0 + 2) + rr) * 16 + 2 * (sub & 3)) = sl;
     }
     if (lane == 0) *(float*)(fb + 1088 * 16 + 4 * rr) = ldexpf(1.0f, -ex);
 }

@@ -146,7 +146,6 @@ int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream
 //          qs[32g .. 32g+15] of row j, then qs[32g+16 .. 32g+31].  Every load
 //          of a wave is one contiguous 256- or 1024-byte run.
 struct WTile { uint4 hdr, qa, qb; };
-struct ActOp { half8_t h[8], l[8], ys; };
 
 __device__ __forceinline__ void load_wtile(WTile& w, const uint8_t* blk, int g) {
     w.hdr = *(const uint4*)blk;
@@ -178,8 +177,8 @@ __device__ __forceinline__ WScale q4k_wscale(const WTile& w, int g) {
     c.lo_add = c.sc * (_Float16)-1024.0f;
     c.hi_mul = c.sc * (_Float16)0.0625f;
     c.hi_add = c.sc * (_Float16)-64.0f;
-    // mins of sub-blocks 4g..4g+3 for g < 2 (groups 2, 3 carry the zero padding
-    // on the activation side, so their values do not matter)
+    // mins of sub-blocks 4(g&1) .. +3: lane groups 0, 1 meet the hi halves of
+    // the activation sub-block sums, groups 2, 3 the lo halves (act16.h)
     const uint32_t mw = (g & 1) ? sb.mn_hi : sb.mn_lo;
     const half2_t m01 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04010400u)) + k1024;
     const half2_t m23 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, mw, 0x04030402u)) + k1024;
@@ -210,55 +209,6 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
     p2 = __builtin_elementwise_fma(p2, mul, add);
     p3 = __builtin_elementwise_fma(p3, mul, add);
     return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
-}
-
-// Dequantised B operand of one weight tile and block: q * sc for the 8 K
-// steps, the sub-block mins, d and 64 * dmin.
-struct WOp { half8_t b[8]; half4_t bmin; float d, dmin64; };
-
-__device__ __forceinline__ WOp q4k_wop(const WTile& w, int g) {
-    WOp B;
-    const WScale c = q4k_wscale(w, g);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) B.b[t] = q4k_bop(w, c, t);
-    B.bmin = c.bmin;
-    B.d = c.d;
-    B.dmin64 = c.dmin64;
-    return B;
-}
-
-// One block of one weight tile against one activation tile (before the
-// block's activation scale): d * sum_s sc_s sum q x - 64 dmin * sum_s mn_s ys_s.
-__device__ __forceinline__ floatx4 q4k_mma(const WOp& B, const ActOp& A, int g) {
-    floatx4 am = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.h[t], B.b[t], am, 0, 0, 0);
-        am = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.l[t], B.b[t], am, 0, 0, 0);
-    }
-    const _Float16 z = (_Float16)0.f;
-    const bool on = g < 2;
-    const half4_t ysh = {on ? A.ys[0] : z, on ? A.ys[2] : z, on ? A.ys[4] : z, on ? A.ys[6] : z};
-    const half4_t ysl = {on ? A.ys[1] : z, on ? A.ys[3] : z, on ? A.ys[5] : z, on ? A.ys[7] : z};
-    floatx4 an = {0.f, 0.f, 0.f, 0.f};
-    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, B.bmin, an, 0, 0, 0);
-    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, B.bmin, an, 0, 0, 0);
-    floatx4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = B.d * am[i] - B.dmin64 * an[i];
-    return r;
-}
-
-// Activation operand of one tile-block from its staged units.
-__device__ __forceinline__ void load_act_units(ActOp& A, floatx4& rs, const uint4* sa, int lane) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        A.h[t] = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
-        A.l[t] = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
-    }
-    A.ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
-    const float4 rv = __builtin_bit_cast(float4, sa[1088 + (lane >> 4)]);
-    rs = floatx4{rv.x, rv.y, rv.z, rv.w};
 }
 
 // Decode kernel (one 16-row activation tile).  A workgroup of four waves
@@ -358,18 +308,13 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
                     am[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bop, am[r], 0, 0, 0);
                 }
             }
-            const half8_t ys = __builtin_bit_cast(half8_t, cur[1024 + lane]);
+            const half4_t ys = *(const half4_t*)(cur + 1024 + lane);
             const float4 rv = __builtin_bit_cast(float4, cur[1088 + g]);
             const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
-            const _Float16 z = (_Float16)0.f;
-            const bool on = g < 2;
-            const half4_t ysh = {on ? ys[0] : z, on ? ys[2] : z, on ? ys[4] : z, on ? ys[6] : z};
-            const half4_t ysl = {on ? ys[1] : z, on ? ys[3] : z, on ? ys[5] : z, on ? ys[7] : z};
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 floatx4 an = {0.f, 0.f, 0.f, 0.f};
-                an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, cs[r].bmin, an, 0, 0, 0);
-                an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, cs[r].bmin, an, 0, 0, 0);
+                an = __builtin_amdgcn_mfma_f32_16x16x16f16(ys, cs[r].bmin, an, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[r][i] += (cs[r].d * am[r][i] - cs[r].dmin64 * an[i]) * rs[i];
             }
@@ -507,21 +452,16 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
                     }
                 }
             }
-            const _Float16 z = (_Float16)0.f;
-            const bool on = g < 2;
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
                 const uint4* sa = cur + n * ACT_FRAG_UNITS;
-                const half8_t ys = __builtin_bit_cast(half8_t, sa[1024 + lane]);
+                const half4_t ys = *(const half4_t*)(sa + 1024 + lane);
                 const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
                 const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
-                const half4_t ysh = {on ? ys[0] : z, on ? ys[2] : z, on ? ys[4] : z, on ? ys[6] : z};
-                const half4_t ysl = {on ? ys[1] : z, on ? ys[3] : z, on ? ys[5] : z, on ? ys[7] : z};
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     floatx4 an = {0.f, 0.f, 0.f, 0.f};
-                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysh, cs[r].bmin, an, 0, 0, 0);
-                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ysl, cs[r].bmin, an, 0, 0, 0);
+                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ys, cs[r].bmin, an, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         acc[r][n][i] += (cs[r].d * am[r][n][i] - cs[r].dmin64 * an[i]) * rs[i];
