@@ -435,11 +435,17 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
 #pragma unroll
                 for (int n = 0; n < NT; ++n) am[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
+            // the B operands of K step t + 1 are built while step t's MFMAs run
+            half8_t bcur[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) bcur[r] = q4k_bop(wc[r], cs[r], 0);
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                half8_t bop[R];
+                half8_t bnx[R];
+                if (t < 7) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) bop[r] = q4k_bop(wc[r], cs[r], t);
+                    for (int r = 0; r < R; ++r) bnx[r] = q4k_bop(wc[r], cs[r], t + 1);
+                }
 #pragma unroll
                 for (int n = 0; n < NT; ++n) {
                     const uint4* sa = cur + n * ACT_FRAG_UNITS;
@@ -447,9 +453,13 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
                     const half8_t l = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
-                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bop[r], am[r][n], 0, 0, 0);
-                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bop[r], am[r][n], 0, 0, 0);
+                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bcur[r], am[r][n], 0, 0, 0);
+                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bcur[r], am[r][n], 0, 0, 0);
                     }
+                }
+                if (t < 7) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) bcur[r] = bnx[r];
                 }
             }
 #pragma unroll
@@ -568,8 +578,11 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
     const int act_tiles = a.rows_pad / 16;
     if (act_tiles > 1) {
         // prefill: all tensors in one launch, NT activation tiles per
-        // workgroup; the split count minimises the rounds of workgroups per
-        // unit of work (a last, partly filled round idles the chip)
+        // workgroup; the split count minimises rounds of workgroups x (blocks
+        // per workgroup + a fixed cost of about four blocks for the
+        // workgroup's set-up, staging prologue and partial stores), a last,
+        // partly filled round costing a whole one (measured at T = 320: two
+        // splits beat 8 and 14 on the 4096-row shapes by 8-14 %)
         const int NT = act_tiles >= 4 ? 4 : 2;
         Q4kTargets tg{};
         int wgs = 0;
@@ -588,8 +601,8 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         double best = 1e30;
         for (int c = 1; c <= 16 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
             const int rounds = (tasks * c + slots - 1) / slots;
-            const double cost = (double)rounds / c;
-            if (cost < best - 1e-9) { best = cost; S = c; }
+            const double cost = (double)rounds * ((double)(nblk + c - 1) / c + 4.0);
+            if (cost <= best + 1e-9) { best = cost; S = c; }   // ties: more splits (measured faster)
         }
         static const int S_env = env_int("SLATE_HIP_Q4K_PF_S", 0);
         if (S_env > 0) S = std::min(S_env, std::max(1, std::min(max_splits, nblk)));

@@ -434,15 +434,17 @@ int launch_q8(const Q4kTarget* t, int n, const Act8& a, float* out, int64_t ldo,
             }
         }
     } else {
-        // the split count that minimises rounds of workgroups per unit of
-        // work (a last, partly filled round idles the chip)
+        // the split count that minimises rounds of workgroups x (groups per
+        // workgroup + a fixed cost of about four groups per workgroup), a
+        // last, partly filled round costing a whole one (the Q4_K prompt
+        // planner's model)
         const int NT = act_tiles >= 4 ? 4 : 2;
         const int tasks = (q8_targets(t, n, 2).grp_end + 7) / 8 * ((act_tiles + NT - 1) / NT);
         const int per_cu = (160 * 1024) / (2 * NT * ACT8_UNITS * 16);
         const int slots = cu_count() * std::max(1, per_cu);
         double best = 1e30;
         for (int c = 1; c <= 16 && c <= s_cap; c *= 2) {
-            const double cost = (double)((tasks * c + slots - 1) / slots) / c;
+            const double cost = (double)((tasks * c + slots - 1) / slots) * ((double)(ngrp + c - 1) / c + 4.0);
             if (cost < best - 1e-9) { best = cost; S = c; }
         }
     }
