@@ -6,7 +6,9 @@
 // units at frag + (rt * K/256 + kb) * ACT_FRAG_UNITS, ordered exactly as the
 // MFMA lanes read them (lane = 16 * g + j: row j of the tile, lane group g):
 //   unit (2t + h) * 64 + lane : x*s hi (h = 0) / lo (h = 1), elements
-//                               64g + 8t .. +7 of the block
+//                               64g + 8t + {0, 2, 1, 3, 4, 6, 5, 7} of the
+//                               block (the order of the weight operand,
+//                               k_q4k.hip q4k_bop)
 //   unit 1024 + lane          : bytes 0..7, four halves: for g < 2 the hi
 //                               parts of the sums of sub-blocks 4g .. 4g+3,
 //                               for g >= 2 the lo parts of sub-blocks
@@ -53,8 +55,9 @@ __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb,
     const int rr = r & 15;
     uint8_t* fb = (uint8_t*)a.frag + ((size_t)(r >> 4) * (a.K / QK) + kb) * ACT_FRAG_UNITS * 16;
     const int g = lane >> 4, t = (lane >> 1) & 7, half_off = 8 * (lane & 1);
-    *(act_half4_t*)(fb + ((2 * t) * 64 + 16 * g + rr) * 16 + half_off) = h;
-    *(act_half4_t*)(fb + ((2 * t + 1) * 64 + 16 * g + rr) * 16 + half_off) = l;
+    const act_half4_t hp = {h[0], h[2], h[1], h[3]}, lp = {l[0], l[2], l[1], l[3]};
+    *(act_half4_t*)(fb + ((2 * t) * 64 + 16 * g + rr) * 16 + half_off) = hp;
+    *(act_half4_t*)(fb + ((2 * t + 1) * 64 + 16 * g + rr) * 16 + half_off) = lp;
     if ((lane & 7) == 0) {
         // sub-block s: hi half in lane group s>>2, lo half in lane group
         // (s>>2) + 2, both as element s&3 of the unit

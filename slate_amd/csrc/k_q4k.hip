@@ -188,22 +188,35 @@ __device__ __forceinline__ WScale q4k_wscale(const WTile& w, int g) {
     return c;
 }
 
-// B operand of K step t: q * sc exact in f16 (q <= 15, sc <= 63), built from
-// 1024+q (low nibble) or 1024+16q (high nibble) by v_perm and one exact fma.
+// B operand of K step t: q * sc exact in f16 (q <= 15, sc <= 63), built
+// from 1024+q (low nibble) or 1024+16q (high nibble) by one v_and_or per
+// two values (the nibbles of bytes 0 and 2 of a dword, then of bytes 1 and
+// 3 after an 8-bit shift that the low- and high-nibble steps share) and one
+// exact fma.  Element order within the lane's 8 values: 0, 2, 1, 3, 4, 6,
+// 5, 7 -- the activation operand is stored in the same order (act16.h).
+// (x & m) | k in one v_and_or_b32 (the compiler splits it when m and k are
+// both literals: one VOP3 instruction takes one literal); m in an SGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t k) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(k));
+    return r;
+}
+
 __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int t) {
     const uint4 Q = t < 4 ? w.qa : w.qb;
     const int tq = t & 3;
-    const uint32_t mask = (tq & 2) ? 0xf0f0f0f0u : 0x0f0f0f0fu;
-    const uint32_t w0 = ((tq & 1) ? Q.z : Q.x) & mask;
-    const uint32_t w1 = ((tq & 1) ? Q.w : Q.y) & mask;
+    const uint32_t q0 = (tq & 1) ? Q.z : Q.x;
+    const uint32_t q1 = (tq & 1) ? Q.w : Q.y;
+    const uint32_t mask = (tq & 2) ? 0x00f000f0u : 0x000f000fu;
+    const uint32_t k1024 = 0x64006400u;
     const half2_t mv = (tq & 2) ? c.hi_mul : c.sc;
     const half2_t av = (tq & 2) ? c.hi_add : c.lo_add;
     const _Float16 m = t < 4 ? mv.x : mv.y, a = t < 4 ? av.x : av.y;
     const half2_t mul = {m, m}, add = {a, a};
-    half2_t p0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u));
-    half2_t p1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u));
-    half2_t p2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u));
-    half2_t p3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u));
+    half2_t p0 = __builtin_bit_cast(half2_t, and_or(q0, mask, k1024));
+    half2_t p1 = __builtin_bit_cast(half2_t, and_or(q0 >> 8, mask, k1024));
+    half2_t p2 = __builtin_bit_cast(half2_t, and_or(q1, mask, k1024));
+    half2_t p3 = __builtin_bit_cast(half2_t, and_or(q1 >> 8, mask, k1024));
     p0 = __builtin_elementwise_fma(p0, mul, add);
     p1 = __builtin_elementwise_fma(p1, mul, add);
     p2 = __builtin_elementwise_fma(p2, mul, add);
