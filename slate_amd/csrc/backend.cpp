@@ -369,7 +369,9 @@ int slate_hip_argmax_rows(int32_t* out, const float* logits, int B, int V) {
     if (!ensure()) return -7;
     SH_REQUIRE(out && logits && B > 0 && V > 0, "argmax_rows: bad arguments");
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
-    return launch_argmax_rows(out, logits, B, V, g_stream);
+    void* ws = scratch(6, argmax_workspace_bytes(B, V));
+    if (!ws) return -2;
+    return launch_argmax_rows(out, logits, B, V, ws, g_stream);
 }
 
 struct RopeTable { float* dev = nullptr; int max_pos = 0; };

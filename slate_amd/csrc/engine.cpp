@@ -85,6 +85,7 @@ struct slate_hip_llama {
     int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
             *last_tok = nullptr, *status = nullptr, *next = nullptr;
     int64_t* kv_base = nullptr;
+    void* argmax_ws = nullptr;     // (value, index) per row and chunk of the greedy argmax
     // Per-step host input, uploaded in one copy: [slot|pos0|n_new (max_slots
     // each)] [tokens (T)] [decode query blocks (n_dec)] [prefill block first
     // tokens (n_pre)] [prefill block sizes (n_pre)]; d_desc mirrors it.
@@ -184,7 +185,8 @@ int alloc_runtime(slate_hip_llama* m) {
     if (dalloc(m, &m->x, T * D) || dalloc(m, &m->xn, T * D) || dalloc(m, &m->q, T * D) ||
         dalloc(m, &m->att, T * D) || dalloc(m, &m->h, T * H) || dalloc(m, &m->xlast, (size_t)m->max_slots * D) ||
         // the LM-head matmul writes whole 16-row tiles
-        dalloc(m, &m->logits, (size_t)row_pad(m->max_slots) * c.vocab))
+        dalloc(m, &m->logits, (size_t)row_pad(m->max_slots) * c.vocab) ||
+        dalloc(m, (char**)&m->argmax_ws, argmax_workspace_bytes(m->max_slots, c.vocab)))
         return -2;
     const int W = std::max({D + 2 * kvd, 2 * H, D});
     m->part_floats = (size_t)std::max<size_t>(16 * 64, T) * W;
@@ -592,7 +594,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     // rows of each sequence's last token -> xlast (gather by last_tok)
     if ((rc = launch_embed_rows(m->xlast, m->xn, m->last_tok, n, T, D, s))) return rc;
     if ((rc = lm_head(m, n, s))) return rc;
-    if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, s))) return rc;
+    if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, m->argmax_ws, s))) return rc;
     SH_CHECK_HIP(hipMemcpyAsync(m->h_next, m->next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
     SH_CHECK_HIP(hipMemcpyAsync(m->h_status, m->status, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     if (m->prof_on) m->prof_recs.push_back({m->step_mixed ? 5 : 2, 0.0, estep, prof_mark(m, s)});

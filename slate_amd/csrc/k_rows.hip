@@ -442,54 +442,82 @@ int launch_rope_kv(float* qout, void* Kpool, void* Vpool, const float* part, int
 // ---------------------------------------------------------------------------
 // Greedy argmax per row with sampling.c:14-18 semantics: the first maximal
 // element wins (strict '>'), NaN is never selected unless element 0 is NaN,
-// in which case nothing compares greater and index 0 is returned.  1024
-// threads per row; thread i scans float4 groups i, i + 1024, ... in order,
-// then a tree keeps the larger value, or the lower index on ties.
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(int32_t* __restrict__ out,
-                                                           const float* __restrict__ logits, int V) {
-    __shared__ float sv[1024];
-    __shared__ int si[1024];
-    const float* p = logits + (size_t)blockIdx.x * V;
-    const int tid = threadIdx.x;
-    float bv = -INFINITY;
-    int bi = -1;
-    auto take = [&](float v, int i) {
-        if (v > bv || (bi < 0 && !(v != v))) { bv = v; bi = i; }
-    };
-    const bool al = ((uintptr_t)p & 15) == 0;
-    const int nv4 = al ? V / 4 : 0;
-#pragma unroll 4
-    for (int q = tid; q < nv4; q += 1024) {
-        const float4 v = *(const float4*)(p + 4 * q);
-        take(v.x, 4 * q);
-        take(v.y, 4 * q + 1);
-        take(v.z, 4 * q + 2);
-        take(v.w, 4 * q + 3);
-    }
-    for (int i = 4 * nv4 + tid; i < V; i += 1024) take(p[i], i);
-    sv[tid] = bv;
-    si[tid] = bi;
-    __syncthreads();
-    for (int o = 512; o > 0; o >>= 1) {
-        if (tid < o) {
-            float v2 = sv[tid + o];
-            int i2 = si[tid + o];
-            float v1 = sv[tid];
-            int i1 = si[tid];
-            bool tk = i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 < i1));
-            if (tk) { sv[tid] = v2; si[tid] = i2; }
+// in which case nothing compares greater and index 0 is returned.
+// Two passes: chunks of ARGMAX_CHUNK elements of every row in parallel (a
+// thread scans its elements in index order, then a tree keeps the larger
+// value, or the lower index on ties; NaN never enters), then one wave per
+// row combines its chunks the same way.  ws holds (value, index) per
+// (row, chunk).
+constexpr int ARGMAX_CHUNK = 4096;
+struct AmBest { float v; int i; };
+__device__ __forceinline__ void am_take(AmBest& b, float v, int i) {
+    if (v > b.v || (b.i < 0 && !(v != v))) { b.v = v; b.i = i; }
+}
+__device__ __forceinline__ AmBest am_pick(AmBest a, AmBest b) {   // a before b in index order
+    const bool tk = b.i >= 0 && (a.i < 0 || b.v > a.v || (b.v == a.v && b.i < a.i));
+    return tk ? b : a;
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(float2* __restrict__ ws,
+                                                          const float* __restrict__ logits, int V, int nch) {
+    __shared__ AmBest sb[256];
+    const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const float* p = logits + (size_t)r * V;
+    const int e0 = c * ARGMAX_CHUNK, e1 = min(e0 + ARGMAX_CHUNK, V);
+    AmBest bst{-INFINITY, -1};
+    if (((uintptr_t)(p + e0) & 15) == 0 && e1 - e0 == ARGMAX_CHUNK) {
+        float4 v[ARGMAX_CHUNK / 1024];
+#pragma unroll
+        for (int k = 0; k < ARGMAX_CHUNK / 1024; ++k) v[k] = *(const float4*)(p + e0 + 4 * (tid + 256 * k));
+#pragma unroll
+        for (int k = 0; k < ARGMAX_CHUNK / 1024; ++k) {
+            const int i = e0 + 4 * (tid + 256 * k);
+            am_take(bst, v[k].x, i);
+            am_take(bst, v[k].y, i + 1);
+            am_take(bst, v[k].z, i + 2);
+            am_take(bst, v[k].w, i + 3);
         }
+    } else {
+        for (int i = e0 + tid; i < e1; i += 256) am_take(bst, p[i], i);
+    }
+    sb[tid] = bst;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) sb[tid] = am_pick(sb[tid], sb[tid + o]);
         __syncthreads();
     }
-    if (tid == 0) {
-        float p0 = p[0];
-        out[blockIdx.x] = (p0 != p0 || si[0] < 0) ? 0 : si[0];
+    if (tid == 0) ws[(size_t)r * nch + c] = make_float2(sb[0].v, __int_as_float(sb[0].i));
+}
+
+__global__ __launch_bounds__(64) void argmax_fin_kernel(int32_t* __restrict__ out, const float2* __restrict__ ws,
+                                                        const float* __restrict__ logits, int V, int nch) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    AmBest bst{-INFINITY, -1};
+    for (int c = lane; c < nch; c += 64) {            // chunks in index order per lane
+        const float2 w = ws[(size_t)r * nch + c];
+        bst = am_pick(bst, AmBest{w.x, __float_as_int(w.y)});
+    }
+    for (int o = 1; o < 64; o <<= 1) {                // lane-order tree: the lower lane is earlier
+        const float ov = __shfl_down(bst.v, o, 64);
+        const int oi = __shfl_down(bst.i, o, 64);
+        if ((lane & (2 * o - 1)) == 0 && lane + o < 64) bst = am_pick(bst, AmBest{ov, oi});
+    }
+    if (lane == 0) {
+        const float p0 = logits[(size_t)r * V];
+        out[r] = (p0 != p0 || bst.i < 0) ? 0 : bst.i;
     }
 }
 
-int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, hipStream_t s) {
+size_t argmax_workspace_bytes(int B, int V) {
+    return (size_t)B * ((V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK) * sizeof(float2);
+}
+
+int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, void* ws, hipStream_t s) {
     if (B <= 0) return 0;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(B), dim3(1024), 0, s, out, logits, V);
+    if (!ws || V <= 0) { set_error(-1, "argmax: bad arguments"); return -1; }
+    const int nch = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(nch, B), dim3(256), 0, s, (float2*)ws, logits, V, nch);
+    hipLaunchKernelGGL(argmax_fin_kernel, dim3(B), dim3(64), 0, s, out, (const float2*)ws, logits, V, nch);
     SH_CHECK_LAUNCH();
     return 0;
 }

@@ -290,6 +290,25 @@ def test_argmax_rows(hip, orc):
     out2 = DB(8)
     check(hip.argmax_rows(out2.p, dev(L2).p, 2, 10), "argmax")
     assert list(host(out2, np.int32, 2)) == [0, 0]
+    # rows are reduced in chunks of 4096: a NaN opening a chunk must not hide
+    # that chunk's maximum, equal maxima in different chunks keep the first,
+    # an all -inf row gives 0, and an odd row length (rows not 16-byte
+    # aligned) takes the scalar path
+    for V3 in (128256, 8197):
+        L3 = rng.integers(-1000, 1000, (5, V3)).astype(np.float32)
+        L3[0, 4096] = np.nan
+        L3[0, 4100] = 5000.0
+        L3[1, 1000] = 3000.0
+        L3[1, V3 - 2] = 3000.0
+        L3[2, :] = -np.inf
+        L3[3, V3 - 1] = 4000.0
+        L3[4, 0] = -np.inf
+        L3[4, 1:] = np.nan
+        out3 = DB(5 * 4)
+        check(hip.argmax_rows(out3.p, dev(L3).p, 5, V3), "argmax")
+        want3 = [orc.lib.orc_argmax(fp(np.ascontiguousarray(L3[b])), V3) for b in range(5)]
+        assert want3[0] == 4100 and want3[1] == 1000 and want3[2] == 0 and want3[3] == V3 - 1 and want3[4] == 0
+        assert list(host(out3, np.int32, 5)) == want3
 
 
 def test_pack_batch_bitexact(orc):
