@@ -249,19 +249,30 @@ __global__ __launch_bounds__(1024) void rmsnorm_act_kernel(float* __restrict__ y
     const int r = blockIdx.x;
     const int nt = blockDim.x, tid = threadIdx.x, lane = tid & 63;
     const bool valid = r < rows;
-    float4 v[RMS_MAX_CHUNKS];
-    float acc = 0.f;
+    // every load (x, w, the first eight partials of each chunk) is issued
+    // before any arithmetic; x is written back after the row reduction
+    float4 v[RMS_MAX_CHUNKS], wv[RMS_MAX_CHUNKS];
+    Split4 pre[RMS_MAX_CHUNKS];
 #pragma unroll
     for (int c = 0; c < RMS_MAX_CHUNKS; ++c) {
         v[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[c] = v[c];
         const int e = 4 * (tid + nt * c);
         if (valid && e < D) {
-            float* xr = x + (size_t)r * D + e;
-            float4 xv = *(const float4*)xr;
+            v[c] = *(const float4*)(x + (size_t)r * D + e);
+            wv[c] = *(const float4*)(w + e);
+            if (delta) pre[c] = split_load4(delta + (size_t)r * D + e, nsplit, split_stride);
+        }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < RMS_MAX_CHUNKS; ++c) {
+        const int e = 4 * (tid + nt * c);
+        if (valid && e < D) {
+            float4 xv = v[c];
             if (delta) {
-                const float4 sm = split_sum4(delta + (size_t)r * D + e, nsplit, split_stride);
+                const float4 sm = split_fin4(pre[c], delta + (size_t)r * D + e, nsplit, split_stride);
                 xv.x += sm.x; xv.y += sm.y; xv.z += sm.z; xv.w += sm.w;
-                *(float4*)xr = xv;
             }
             v[c] = xv;
             acc = __builtin_fmaf(xv.x, xv.x, acc);
@@ -283,9 +294,9 @@ __global__ __launch_bounds__(1024) void rmsnorm_act_kernel(float* __restrict__ y
         if (e >= D) break;                        // uniform per wave when D % 256 == 0
         float4 yv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (valid) {
-            const float4 wv = *(const float4*)(w + e);
-            yv = make_float4((v[c].x * wv.x) * inv, (v[c].y * wv.y) * inv, (v[c].z * wv.z) * inv,
-                             (v[c].w * wv.w) * inv);
+            if (delta) *(float4*)(x + (size_t)r * D + e) = v[c];
+            yv = make_float4((v[c].x * wv[c].x) * inv, (v[c].y * wv[c].y) * inv, (v[c].z * wv[c].z) * inv,
+                             (v[c].w * wv[c].w) * inv);
             if (y) *(float4*)(y + (size_t)r * D + e) = yv;
         }
         if (act) act16_store_block(a, r, e / QK, lane, yv);
