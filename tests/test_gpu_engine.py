@@ -402,3 +402,87 @@ def test_mixed_dtype_groups_match_oracle(orc):
     prompts = [rng.integers(0, MIXQ.vocab, n).astype(np.int32) for n in (9, 1, 30)]
     m = slate_amd.Llama.from_tensors(MIXQ, t, max_slots=4, max_tokens=48)
     replay_against_oracle(orc, MIXQ, t, m, prompts, 4)
+
+
+def device_model_tensors(m, shape):
+    """Host copy of a device-built model in the make_llama layout (for the oracle)."""
+    t = {}
+
+    def get(name, key, shp):
+        raw, dt = m.get_tensor(name)
+        t[key] = (raw.view(np.float32) if dt == 0 else raw, dt, shp)
+
+    D, kvd, H = shape.d_model, shape.kv_dim, shape.ffn
+    get("token_embd", "token_embd.weight", (shape.vocab, D))
+    get("output_norm", "output_norm.weight", (D,))
+    get("output", "output.weight", (shape.vocab, D))
+    dims = {"attn_q": (D, D), "attn_k": (kvd, D), "attn_v": (kvd, D), "attn_output": (D, D),
+            "ffn_gate": (H, D), "ffn_up": (H, D), "ffn_down": (D, H)}
+    for i in range(shape.n_layers):
+        for n in ("attn_norm", "ffn_norm"):
+            get(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", (D,))
+        for n, shp in dims.items():
+            get(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", shp)
+    return t
+
+
+def test_70b_layer_shapes_match_oracle(orc):
+    """LLaMA-3-70B layer shapes (d 8192, 64 q / 8 kv heads, so 8 q heads per
+    kv head, SwiGLU 28672), all Q4_K, two layers and a small vocabulary so
+    the CPU reference stays within seconds: a ragged prompt step, then decode
+    steps, each against the oracle."""
+    shape = LlamaShape(n_layers=2, d_model=8192, n_heads=64, n_kv_heads=8, ffn=28672, vocab=512, max_seq=256)
+    m = slate_amd.Llama.synthetic(shape, seed=70, quant=18, max_slots=3, max_tokens=64)
+    rng = np.random.default_rng(70)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (9, 3)]
+    sess = [m.session() for _ in prompts]
+    rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+    assert rc == 0 and np.all(np.isfinite(lg))
+    steps = [lg]
+    toks = np.asarray(nxt, np.int32)
+    for _ in range(2):
+        rc, lg, nxt = m.step(sess, [1, 1], toks)
+        assert rc == 0
+        steps.append(lg)
+        toks = np.asarray(nxt, np.int32)
+    om = OracleModel(orc, shape, device_model_tensors(m, shape))
+    for i, p in enumerate(prompts):
+        o = om.session()
+        rc, want = o.prefill(p)
+        assert rc == 0 and relerr(steps[0][i], want) < TOL
+        tok = int(np.argmax(steps[0][i]))
+        for k in range(1, len(steps)):
+            rc, want = o.decode(tok)
+            assert rc == 0 and relerr(steps[k][i], want) < TOL, (i, k)
+            tok = int(np.argmax(steps[k][i]))
+
+
+def test_70b_shape_full_depth_runs_and_is_batch_invariant():
+    """The LLaMA-3-70B-shaped model at full size (80 layers, d 8192, 64 / 8
+    heads, SwiGLU 28672, vocabulary 128256; ~39 GB of Q4_K): a mixed ragged
+    step and decode steps give one sequence the logits it gets alone, within
+    1e-4 (test_batched_equals_sequential's bound: a 56-token step and a
+    30-token prefill split K differently, and the rounding of the two sums
+    compounds over 80 layers -- 2e-5 measured)."""
+    shape = LlamaShape(n_layers=80, d_model=8192, n_heads=64, n_kv_heads=8, ffn=28672, vocab=128256,
+                       max_seq=512)
+    m = slate_amd.Llama.synthetic(shape, seed=71, quant=18, max_slots=5, max_tokens=64)
+    rng = np.random.default_rng(71)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (30, 7, 19)]
+    sess = [m.session() for _ in prompts]
+    rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+    assert rc == 0 and np.all(np.isfinite(lg))
+    solo = m.session()
+    rc, lg1 = solo.prefill(prompts[0])
+    assert rc == 0 and relerr(lg1, lg[0]) < 1e-4
+    toks = list(nxt)
+    for _ in range(3):
+        rc, lg, nxt = m.step(sess, [1] * 3, toks)
+        rc2, l2 = solo.decode(toks[0])
+        assert rc == 0 and rc2 == 0 and np.all(np.isfinite(lg))
+        assert relerr(l2, lg[0]) < 1e-4
+        toks = list(nxt)
+    solo.free()
+    for s in sess:
+        s.free()
+    m.free()
