@@ -224,8 +224,8 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
     return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-// Decode kernel (one 16-row activation tile).  A workgroup of four waves
-// owns 4R weight tiles (possibly spread over up to three fused tensors) and
+// Decode kernel (one 16-row activation tile).  A workgroup of WAVES waves
+// owns WAVES*R weight tiles (possibly spread over up to three fused tensors) and
 // one split of super-blocks.  The activation units of a block are copied
 // into a double-buffered LDS tile by direct global->LDS loads, one block
 // ahead and issued before the next block's weight loads; each wave holds its
@@ -233,9 +233,10 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
 // one wait for all loads and one barrier.  W and frag are not __restrict__:
 // loads through restrict pointers count as invariant and may be moved across
 // the barriers that order them here.
-template <int R, bool TILED>
-__global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4* frag, float* __restrict__ out,
-                                                      int64_t ldo, int64_t split_stride, int nblk, int bps) {
+template <int R, bool TILED, int WAVES = 4>
+__global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, const uint4* frag,
+                                                             float* __restrict__ out, int64_t ldo,
+                                                             int64_t split_stride, int nblk, int bps) {
     __shared__ uint4 s_act[2 * ACT_FRAG_UNITS];
     constexpr int CHUNKS = ACT_FRAG_UNITS / 64;       // 1 KiB wave copies per block
     const int tid = threadIdx.x;
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
     // wave-uniform (SGPR): the tensor selection and every weight and operand
     // base address below are scalar; loads add the lane's offset
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = blockIdx.x * 4 + wv;
+    const int grp = blockIdx.x * WAVES + wv;
     const int ti = (tg.n > 2 && grp >= tg.grp0[2]) ? 2 : ((tg.n > 1 && grp >= tg.grp0[1]) ? 1 : 0);
     const uint8_t* W = ti == 2 ? tg.w[2] : (ti == 1 ? tg.w[1] : tg.w[0]);
     const int M = ti == 2 ? tg.M[2] : (ti == 1 ? tg.M[1] : tg.M[0]);
@@ -272,8 +273,8 @@ __global__ __launch_bounds__(256) void q4k_dec_kernel(Q4kTargets tg, const uint4
     auto stage = [&](uint4* dst, int kb) {
         const uint4* src = frag + (size_t)kb * ACT_FRAG_UNITS;
 #pragma unroll
-        for (int i = 0; i < (CHUNKS + 3) / 4; ++i) {
-            const int c = wv + 4 * i;
+        for (int i = 0; i < (CHUNKS + WAVES - 1) / WAVES; ++i) {
+            const int c = wv + WAVES * i;
             if (c < CHUNKS) lds_copy16(src + c * 64, o_act, lds_addr(dst + c * 64));
         }
     };
@@ -523,10 +524,18 @@ static int env_int(const char* name, int dflt) {
 // Decode plan: the largest R in {4, 2, 1}, then the fewest splits, that give
 // at least `target` workgroups (about two per CU).  Splits keep >= 2 blocks
 // each: a one-block split never overlaps its weight prefetch with compute.
+// Waves per decode workgroup: 8 by default (measured 2 % faster per decode
+// step than 4, since each staged activation block feeds twice the weight
+// tiles, and 16 was 8 % slower); SLATE_HIP_Q4K_W=4 selects four.
+static int dec_waves() {
+    static const int w = env_int("SLATE_HIP_Q4K_W", 8) == 4 ? 4 : 8;
+    return w;
+}
+
 static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, int* S_out) {
     static const int R_env = env_int("SLATE_HIP_Q4K_R", 0);
     static const int S_env = env_int("SLATE_HIP_Q4K_S", 0);
-    static const int target = env_int("SLATE_HIP_Q4K_WGS", 448);
+    static const int waves_target = env_int("SLATE_HIP_Q4K_WGS", 448) * 4;   // 1792 waves
     if (s_max > nblk / 2) s_max = nblk / 2;
     if (s_max < 1) s_max = 1;
     int R_out_v = (R_env == 1 || R_env == 2 || R_env == 4) ? R_env : 1, S_out_v = s_max;
@@ -536,7 +545,8 @@ static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, i
         int groups = 0;
         for (int i = 0; i < n; ++i) groups += (tiles[i] + R - 1) / R;
         for (int S = 1; S <= s_max; S *= 2) {
-            if ((groups + 3) / 4 * S >= target) {
+            const int W = dec_waves();
+            if ((groups + W - 1) / W * S >= waves_target / W) {
                 R_out_v = R;
                 S_out_v = S;
                 done = true;
@@ -552,6 +562,12 @@ static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, i
 template <int R, bool TILED>
 static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk,
                        int bps, int nsplit, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    if (dec_waves() == 8) {
+        dim3 grid((tg.grp_end + 7) / 8, nsplit);
+        SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8>), grid, dim3(512), 0, s, tg, (const uint4*)a.frag, out, ldo,
+                  ss, nblk, bps);
+        return;
+    }
     dim3 grid((tg.grp_end + 3) / 4, nsplit);
     SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED>), grid, dim3(256), 0, s, tg, (const uint4*)a.frag, out, ldo, ss,
               nblk, bps);
