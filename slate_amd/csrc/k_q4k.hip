@@ -375,6 +375,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     const int j = lane & 15;
     const int g = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // SGPR: scalar staging addresses
+    __builtin_assume(wv >= 0 && wv < WAVES);
     // workgroup x -> tensor (tensors start on workgroup boundaries)
     const int wg = blockIdx.x;
     const int ti = (tg.n > 2 && wg >= tg.grp0[2]) ? 2 : ((tg.n > 1 && wg >= tg.grp0[1]) ? 1 : 0);
@@ -399,18 +400,28 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
         else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
     };
     // copy block kb of activation tiles at0 .. at0+NT-1 (clamped) into `dst`
-    // (every address stays inside the operand buffer: at < act_tiles, kb < nblk)
+    // (every address stays inside the operand buffer: at < act_tiles, kb < nblk).
+    // The wave's chunks sit at fixed byte offsets from block kb's base (the
+    // operand buffer of a prompt chunk is far below 4 GiB) and at fixed LDS
+    // offsets, computed once: a copy costs one 64-bit scalar add and an m0 add.
+    constexpr int NCH = (CHUNKS + WAVES - 1) / WAVES;
     const uint32_t o_act = 16 * lane;
-    auto stage = [&](uint4* dst, int kb) {
+    uint32_t csrc[NCH], clds[NCH];
 #pragma unroll
-        for (int i = 0; i < (CHUNKS + WAVES - 1) / WAVES; ++i) {
-            const int c = wv + WAVES * i;
-            if (c >= CHUNKS) break;
-            const int n = c / (ACT_FRAG_UNITS / 64);
-            const int u = (c - n * (ACT_FRAG_UNITS / 64)) * 64;
-            const int at = min(at0 + n, act_tiles - 1);
-            lds_copy16(frag + ((size_t)at * nblk + kb) * ACT_FRAG_UNITS + u, o_act, lds_addr(dst + n * ACT_FRAG_UNITS + u));
-        }
+    for (int i = 0; i < NCH; ++i) {
+        const int c = min(wv + WAVES * i, CHUNKS - 1);
+        const int n = c / (ACT_FRAG_UNITS / 64);
+        const int u = (c - n * (ACT_FRAG_UNITS / 64)) * 64;
+        const int at = min(at0 + n, act_tiles - 1);
+        csrc[i] = (uint32_t)(((uint32_t)at * (uint32_t)nblk * ACT_FRAG_UNITS + u) * 16u);
+        clds[i] = (uint32_t)((n * ACT_FRAG_UNITS + u) * 16);
+    }
+    auto stage = [&](uint4* dst, int kb) {
+        const char* sb = (const char*)(frag + (size_t)kb * ACT_FRAG_UNITS);
+        const uint32_t lb = lds_addr(dst);
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+            if (wv + WAVES * i < CHUNKS) lds_copy16(sb + csrc[i], o_act, lb + clds[i]);
     };
     WTile wc[R], wn[R];
     floatx4 acc[R][NT];
@@ -606,6 +617,11 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
     if (max_splits < 1) max_splits = 1;
     const int act_tiles = a.rows_pad / 16;
     if (act_tiles > 1) {
+        // the prompt kernel addresses the operand with 32-bit byte offsets
+        if ((double)act_tiles * nblk * ACT_FRAG_UNITS * 16.0 >= 4294967296.0) {
+            set_error(-1, "q4k: activation operand of %d rows x K=%d exceeds 4 GiB", a.rows_pad, a.K);
+            return -1;
+        }
         // prefill: all tensors in one launch, NT activation tiles per
         // workgroup; the split count minimises rounds of workgroups x (blocks
         // per workgroup + a fixed cost of about four blocks for the
