@@ -92,6 +92,7 @@ struct slate_hip_llama {
     int32_t *h_desc = nullptr, *h_tok = nullptr, *h_next = nullptr, *h_status = nullptr;
     int n_dec = 0, n_pre = 0;
     bool step_mixed = false;       // the step carries a prompt chunk (profiling classes)
+    bool step_one_each = false;    // every sequence of the step adds exactly one token
     float* h_logits = nullptr;
     std::vector<int> free_slots;
     std::vector<void*> allocs;
@@ -536,22 +537,33 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
         }
         char* Kl = (char*)m->Kpool + (int64_t)li * m->layer_stride * m->kv_bytes;
         char* Vl = (char*)m->Vpool + (int64_t)li * m->layer_stride * m->kv_bytes;
-        if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd, m->tok2seq,
-                                 m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd, m->head_stride, m->rope_cs,
-                                 rn, m->kv_f16, s)))
-            return rc;
         {
             const Lin* g[1] = {&Ld.o};
             int64_t col[1] = {0};
             const GroupIn gi = group_in(g, 1);
             Act16 a = act_for(m, T, D);
             const size_t ea = m->prof_on ? prof_event(m) : (size_t)-1, eb = m->prof_on ? prof_event(m) : (size_t)-1;
-            if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
-                                              m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
-                                              c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
-                                              m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea), prof_ev(m, eb),
-                                              true, m->kv_f16)))
-                return rc;
+            // one token per sequence: RoPE and the K/V append run inside the
+            // attention kernel; otherwise (prompt chunks) before it
+            rc = 1;
+            if (m->step_one_each)
+                rc = launch_attention_rope(m->att, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
+                                           m->rope_cs, rn, m->tok_pos, T, c.n_heads, c.n_kv_heads, hd,
+                                           m->head_stride, c.max_seq, m->att_po, m->att_pml, gi.q4 ? &a : nullptr, s,
+                                           prof_ev(m, ea), prof_ev(m, eb), m->kv_f16);
+            if (rc < 0) return rc;
+            if (rc > 0) {
+                if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
+                                         m->tok2seq, m->tok_pos, m->kv_base, T, c.n_heads, c.n_kv_heads, hd,
+                                         m->head_stride, m->rope_cs, rn, m->kv_f16, s)))
+                    return rc;
+                if ((rc = launch_attention_blocks(m->att, m->q, Kl, Vl, m->tok2seq, m->tok_pos, m->kv_base, T, d_blk,
+                                                  m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
+                                                  c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
+                                                  m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea),
+                                                  prof_ev(m, eb), true, m->kv_f16)))
+                    return rc;
+            }
             if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
                 m->prof_recs.push_back({m->step_mixed ? 4 : 1, m->step_kv_rows * 2.0 * kvd * 4 + 2.0 * T * D * 4, ea, eb});
             if ((rc = mm_group(m, &a, m->att, T, D, g, col, 1, D, &S, s))) return rc;
@@ -929,6 +941,8 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
         m->n_dec = nd;
         m->n_pre = np;
         m->step_mixed = T > n;
+        m->step_one_each = np == 0 && nd == T && T == n;
+        for (int i = 0; i < n; ++i) m->step_one_each = m->step_one_each && n_new[i] == 1;
     }
     m->step_kv_rows = 0;
     for (int i = 0; i < n; ++i) m->step_kv_rows += (double)sessions[i]->pos + n_new[i];

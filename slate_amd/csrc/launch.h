@@ -57,6 +57,14 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
 // The decode work-unit list that launch_attention_blocks builds (in the tail
 // of the pml buffer) when pairs_ready is false: build it once when several
 // launches share the same tokens and positions (the layers of one step).
+// Decode steps with one token per sequence: RoPE of q and k, the K/V append
+// (what launch_rope_kv does) and the attention of launch_attention_blocks in
+// one kernel plus the merge.  Returns 1, launching nothing, when the shape
+// is not one the fused kernel covers (the caller then runs the two paths).
+int launch_attention_rope(float* out, void* Kp, void* Vp, const float* part, int nsplit, int64_t split_stride,
+                          int qkv_ld, const float* cs, const RowNorm& rn, const int32_t* tok_pos, int T, int Hq,
+                          int Hkv, int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
+                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool kv_f16);
 int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, const int32_t* tok2seq,
                            const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s);
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
