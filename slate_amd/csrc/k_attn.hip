@@ -486,17 +486,34 @@ __device__ __forceinline__ void attn_dec_wave_body(
     const int lg = lane >> 3, ls = lane & 7;
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t base = un.kvb + (int64_t)h * head_stride + (int64_t)k0 * HD;
+    const KVT* Kh = Kp + base;
+    const KVT* Vh = Vp + base;
+    const int kw0 = wv * KW;
+    // with ROPE, the first KP rounds of key rows are loaded before the
+    // prologue where the chunk does not hold key p (its rows are final), so
+    // that their latency overlaps the prologue's
+    constexpr int KP = ROPE ? 2 : 0;
+    float4 kpre[KP > 0 ? KP : 1][NV];
+    auto load_kpre = [&]() {
+        if (kw0 < nk) {
+#pragma unroll
+            for (int it = 0; it < KP; ++it) {
+                const KVT* kr = Kh + (int64_t)min(kw0 + 8 * it + lg, nk - 1) * HD;
+#pragma unroll
+                for (int i = 0; i < NV; ++i) kpre[it][i] = ld_kv4(kr + 32 * i + 4 * ls);
+            }
+        }
+    };
     if constexpr (ROPE) {
         // the unit of the chunk holding key p appends the token's K and V
         // rows; the fence and barrier make them visible to the key loads
         const bool append = p - k0 < ATT_CHUNK;
+        if (!append) load_kpre();
         attn_rope_prologue<HD, G, KVT>(fr, t, h, p, un.kvb + (int64_t)h * head_stride, Hq, Hkv, append, s_q);
         if (append) __threadfence_block();
         __syncthreads();
+        if (append) load_kpre();
     }
-    const KVT* Kh = Kp + base;
-    const KVT* Vh = Vp + base;
-    const int kw0 = wv * KW;
     if (kw0 < nk) {
         const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
         float4 qv[G][NV];
@@ -513,7 +530,7 @@ __device__ __forceinline__ void attn_dec_wave_body(
             const KVT* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
             float4 kv[NV];
 #pragma unroll
-            for (int i = 0; i < NV; ++i) kv[i] = ld_kv4(kr + 32 * i + 4 * ls);
+            for (int i = 0; i < NV; ++i) kv[i] = it < KP ? kpre[it][i] : ld_kv4(kr + 32 * i + 4 * ls);
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 float a = 0.f;
