@@ -237,6 +237,41 @@ def test_q4k_decode_steps_match_oracle(orc):
             tok = int(np.argmax(steps[k][i]))
 
 
+def test_fused_rope_attention_equals_separate_kernels():
+    """Steps in which every sequence adds one token rotate q/k and append K/V
+    inside the decode attention kernel; a step adding several tokens of a
+    sequence runs RoPE/append and attention as separate kernels.  The same
+    tokens fed both ways (four single-token steps, or one step of four tokens
+    per sequence), across the 256-key chunk boundary (positions 254-257, the
+    last a chunk of one key) and beside a short second sequence, give
+    bit-identical final logits and K/V caches: per token the two paths
+    evaluate the same expressions."""
+    shape = LlamaShape(2, 512, 8, 4, 768, 300, 512)
+    t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(21)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (254, 40)]
+    extra = [rng.integers(0, shape.vocab, 4).astype(np.int32) for _ in prompts]
+    out = []
+    for fused in (True, False):
+        m = slate_amd.Llama.from_tensors(shape, t, max_slots=2, max_tokens=512)
+        sess = [m.session() for _ in prompts]
+        rc, _, _ = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts), want_logits=False)
+        assert rc == 0
+        if fused:
+            for k in range(4):
+                rc, lg, _ = m.step(sess, [1, 1], np.array([e[k] for e in extra], np.int32))
+                assert rc == 0
+        else:
+            rc, lg, _ = m.step(sess, [4, 4], np.concatenate(extra))
+            assert rc == 0
+        assert [s.position for s in sess] == [258, 44]
+        out.append((np.array(lg), [s.kv() for s in sess]))
+    (la, kva), (lb, kvb) = out
+    assert np.array_equal(la, lb)
+    for (Ka, Va), (Kb, Vb), n in zip(kva, kvb, (258, 44)):
+        assert np.array_equal(Ka[:, :n], Kb[:, :n]) and np.array_equal(Va[:, :n], Vb[:, :n])
+
+
 def test_graph_replayed_decode_steps_match_eager_launches(golden):
     """Decode-only steps replay a captured HIP graph; interleaved with eager
     prompt steps and repeated many times, every replay gives bit-identical
