@@ -216,7 +216,7 @@ int alloc_runtime(slate_hip_llama* m) {
     const size_t in_ints = 3 * (size_t)S + 4 * T;
     if (dalloc(m, &m->d_desc, in_ints) || dalloc(m, &m->tok_off, S + 1) ||
         dalloc(m, &m->tok2seq, T) || dalloc(m, &m->tok_pos, T) || dalloc(m, &m->last_tok, S) ||
-        dalloc(m, &m->status, 4) || dalloc(m, &m->next, S) || dalloc(m, &m->kv_base, S))
+        dalloc(m, &m->kv_base, S))
         return -2;
     m->d_tok = m->d_desc + 3 * S;
     // index buffers start as valid (all-zero) indices
@@ -233,6 +233,13 @@ int alloc_runtime(slate_hip_llama* m) {
         return -2;
     }
     m->h_tok = m->h_desc + 3 * S;
+    // the packing status and the next-token ids are written by the kernels
+    // straight into pinned host memory: no device-to-host copies per step
+    if (hipHostGetDevicePointer((void**)&m->status, m->h_status, 0) != hipSuccess ||
+        hipHostGetDevicePointer((void**)&m->next, m->h_next, 0) != hipSuccess) {
+        set_error(-7, "engine: pinned host buffers are not device-accessible");
+        return -7;
+    }
     // KV pools start zeroed, like calloc in llama_infer.c:225-226
     if (hipMemset(m->Kpool, 0, kv * m->kv_bytes) != hipSuccess ||
         hipMemset(m->Vpool, 0, kv * m->kv_bytes) != hipSuccess) {
@@ -607,8 +614,6 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if ((rc = launch_embed_rows(m->xlast, m->xn, m->last_tok, n, T, D, s))) return rc;
     if ((rc = lm_head(m, n, s))) return rc;
     if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, m->argmax_ws, s))) return rc;
-    SH_CHECK_HIP(hipMemcpyAsync(m->h_next, m->next, sizeof(int32_t) * n, hipMemcpyDeviceToHost, s));
-    SH_CHECK_HIP(hipMemcpyAsync(m->h_status, m->status, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     if (m->prof_on) m->prof_recs.push_back({m->step_mixed ? 5 : 2, 0.0, estep, prof_mark(m, s)});
     if (want_logits)
         SH_CHECK_HIP(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * (size_t)n * c.vocab,
