@@ -371,7 +371,8 @@ int slate_hip_argmax_rows(int32_t* out, const float* logits, int B, int V) {
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
     void* ws = scratch(6, argmax_workspace_bytes(B, V));
     if (!ws) return -2;
-    return launch_argmax_rows(out, logits, B, V, ws, g_stream);
+    // without a row factor the kernels only read the logits
+    return launch_argmax_rows(out, const_cast<float*>(logits), B, V, ws, g_stream);
 }
 
 struct RopeTable { float* dev = nullptr; int max_pos = 0; };

@@ -468,6 +468,20 @@ int mm_group(slate_hip_llama* m, const Act16* a, const float* X, int T, int K, c
 }
 
 // Final projection for n rows into m->logits [n][V] (single split).
+// Q4_K LM head on a filled operand of its a.rows input rows -> m->logits.
+int lm_head_q4k(slate_hip_llama* m, const Act16& a, hipStream_t s) {
+    const auto& c = m->cfg;
+    const Lin& l = m->out;
+    const size_t e0 = m->prof_on ? prof_event(m) : (size_t)-1, e1 = m->prof_on ? prof_event(m) : (size_t)-1;
+    Q4kTarget t{l.w, c.vocab, 0};
+    int S = 1;
+    const int rc = launch_q4k(&t, 1, true, a, m->logits, c.vocab, 0, 1, &S, s, prof_ev(m, e0), prof_ev(m, e1));
+    if (m->prof_on)
+        m->prof_recs.push_back({a.rows_pad == 16 ? 0 : 3, (double)l.bytes() + 4.0 * a.rows * (c.d_model + c.vocab),
+                                e0, e1});
+    return rc;
+}
+
 int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
     const auto& c = m->cfg;
     const Lin& l = m->out;
@@ -478,14 +492,7 @@ int lm_head(slate_hip_llama* m, int n, hipStream_t s) {
         a.K = c.d_model;
         int rc = launch_act16_from_f32(a, m->xlast, c.d_model, s);
         if (rc) return rc;
-        const size_t e0 = m->prof_on ? prof_event(m) : (size_t)-1, e1 = m->prof_on ? prof_event(m) : (size_t)-1;
-        Q4kTarget t{l.w, c.vocab, 0};
-        int S = 1;
-        rc = launch_q4k(&t, 1, true, a, m->logits, c.vocab, 0, 1, &S, s, prof_ev(m, e0), prof_ev(m, e1));
-        if (m->prof_on)
-            m->prof_recs.push_back({a.rows_pad == 16 ? 0 : 3, (double)l.bytes() + 4.0 * n * (c.d_model + c.vocab), e0,
-                                    e1});
-        return rc;
+        return lm_head_q4k(m, a, s);
     }
     if (l.dtype == DT_Q8_0) {
         Act8 a8 = m->act8;
@@ -607,13 +614,25 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
         }
         S_prev = S;
     }
-    if ((rc = launch_rmsnorm_act(m->xn, m->x, m->part, S_prev, (int64_t)tpad * D, m->out_norm, T, D, c.rms_eps,
-                                 nullptr, s)))
-        return rc;
-    // rows of each sequence's last token -> xlast (gather by last_tok)
-    if ((rc = launch_embed_rows(m->xlast, m->xn, m->last_tok, n, T, D, s))) return rc;
-    if ((rc = lm_head(m, n, s))) return rc;
-    if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, m->argmax_ws, s))) return rc;
+    if (m->step_one_each && m->defer_norm && m->out.dtype == DT_Q4K && D % QK == 0) {
+        // every token is its sequence's last: the residual kernel writes the
+        // LM head operand of x*w directly and the argmax applies the final
+        // RMSNorm factor to the logits (as the deferred norms of the layers)
+        Act16 a = act_for(m, T, D);
+        if ((rc = launch_residual_act(m->x, m->part, S_prev, (int64_t)tpad * D, m->out_norm, T, D, a, m->ssq, s)))
+            return rc;
+        if ((rc = lm_head_q4k(m, a, s))) return rc;
+        const RowNorm rl{m->ssq, D / QK, D, c.rms_eps};
+        if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, m->argmax_ws, s, &rl))) return rc;
+    } else {
+        if ((rc = launch_rmsnorm_act(m->xn, m->x, m->part, S_prev, (int64_t)tpad * D, m->out_norm, T, D,
+                                     c.rms_eps, nullptr, s)))
+            return rc;
+        // rows of each sequence's last token -> xlast (gather by last_tok)
+        if ((rc = launch_embed_rows(m->xlast, m->xn, m->last_tok, n, T, D, s))) return rc;
+        if ((rc = lm_head(m, n, s))) return rc;
+        if ((rc = launch_argmax_rows(m->next, m->logits, n, c.vocab, m->argmax_ws, s))) return rc;
+    }
     if (m->prof_on) m->prof_recs.push_back({m->step_mixed ? 5 : 2, 0.0, estep, prof_mark(m, s)});
     if (want_logits)
         SH_CHECK_HIP(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * (size_t)n * c.vocab,

@@ -469,12 +469,20 @@ __device__ __forceinline__ AmBest am_pick(AmBest a, AmBest b) {   // a before b 
     return tk ? b : a;
 }
 
-__global__ __launch_bounds__(256) void argmax_part_kernel(float2* __restrict__ ws,
-                                                          const float* __restrict__ logits, int V, int nch) {
+// With rn.ssq, the logits are those of a row whose RMSNorm factor was left
+// to the consumer (deferred norm): each is multiplied by the row's factor,
+// written back, and compared scaled.
+__global__ __launch_bounds__(256) void argmax_part_kernel(float2* __restrict__ ws, float* __restrict__ logits,
+                                                          int V, int nch, RowNorm rn) {
     __shared__ AmBest sb[256];
     const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
-    const float* p = logits + (size_t)r * V;
+    float* p = logits + (size_t)r * V;
     const int e0 = c * ARGMAX_CHUNK, e1 = min(e0 + ARGMAX_CHUNK, V);
+    float inv = 1.0f;
+    if (rn.ssq) {
+        const RmsPre rp = row_rms_load(rn.ssq, r, rn.nblk);
+        inv = row_rms_fin(rp, rn.ssq, r, rn.nblk, rn.D, rn.eps);
+    }
     AmBest bst{-INFINITY, -1};
     if (((uintptr_t)(p + e0) & 15) == 0 && e1 - e0 == ARGMAX_CHUNK) {
         float4 v[ARGMAX_CHUNK / 1024];
@@ -483,13 +491,24 @@ __global__ __launch_bounds__(256) void argmax_part_kernel(float2* __restrict__ w
 #pragma unroll
         for (int k = 0; k < ARGMAX_CHUNK / 1024; ++k) {
             const int i = e0 + 4 * (tid + 256 * k);
+            if (rn.ssq) {
+                v[k] = make_float4(v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv);
+                *(float4*)(p + i) = v[k];
+            }
             am_take(bst, v[k].x, i);
             am_take(bst, v[k].y, i + 1);
             am_take(bst, v[k].z, i + 2);
             am_take(bst, v[k].w, i + 3);
         }
     } else {
-        for (int i = e0 + tid; i < e1; i += 256) am_take(bst, p[i], i);
+        for (int i = e0 + tid; i < e1; i += 256) {
+            float v = p[i];
+            if (rn.ssq) {
+                v *= inv;
+                p[i] = v;
+            }
+            am_take(bst, v, i);
+        }
     }
     sb[tid] = bst;
     __syncthreads();
@@ -523,11 +542,12 @@ size_t argmax_workspace_bytes(int B, int V) {
     return (size_t)B * ((V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK) * sizeof(float2);
 }
 
-int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, void* ws, hipStream_t s) {
+int launch_argmax_rows(int32_t* out, float* logits, int B, int V, void* ws, hipStream_t s, const RowNorm* rn) {
     if (B <= 0) return 0;
     if (!ws || V <= 0) { set_error(-1, "argmax: bad arguments"); return -1; }
     const int nch = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
-    hipLaunchKernelGGL(argmax_part_kernel, dim3(nch, B), dim3(256), 0, s, (float2*)ws, logits, V, nch);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(nch, B), dim3(256), 0, s, (float2*)ws, logits, V, nch,
+                       rn ? *rn : RowNorm{});
     hipLaunchKernelGGL(argmax_fin_kernel, dim3(B), dim3(64), 0, s, out, (const float2*)ws, logits, V, nch);
     SH_CHECK_LAUNCH();
     return 0;

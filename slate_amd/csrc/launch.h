@@ -32,8 +32,11 @@ int launch_rope_kv(float* qout, void* Kpool, void* Vpool, const float* part, int
 int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_stride, const float* w, int rows,
                         int D, const Act16& a, float* ssq, hipStream_t s);
 // ws: argmax_workspace_bytes(B, V) of device scratch ((value, index) per row and chunk).
+// rn (deferred RMSNorm of the rows the logits came from): each logit is
+// multiplied by its row's factor in place before the comparison.
 size_t argmax_workspace_bytes(int B, int V);
-int launch_argmax_rows(int32_t* out, const float* logits, int B, int V, void* ws, hipStream_t s);
+int launch_argmax_rows(int32_t* out, float* logits, int B, int V, void* ws, hipStream_t s,
+                       const RowNorm* rn = nullptr);
 int launch_pack_batch(const int32_t* slot, const int32_t* pos0, const int32_t* n_new, int B, int max_seq,
                       int64_t slot_stride, int T_cap, int32_t* tok_off, int32_t* tok2seq,
                       int32_t* tok_pos, int64_t* kv_base, int32_t* last_tok, int32_t* status,

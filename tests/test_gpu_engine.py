@@ -244,8 +244,10 @@ def test_fused_rope_attention_equals_separate_kernels():
     tokens fed both ways (four single-token steps, or one step of four tokens
     per sequence), across the 256-key chunk boundary (positions 254-257, the
     last a chunk of one key) and beside a short second sequence, give
-    bit-identical final logits and K/V caches: per token the two paths
-    evaluate the same expressions."""
+    bit-identical K/V caches (layer 1's rows carry layer 0's attention
+    output): per token the two paths evaluate the same expressions.  The
+    final logits agree within 1e-5: single-token steps also defer the final
+    RMSNorm factor to the argmax, the four-token step normalises the rows."""
     shape = LlamaShape(2, 512, 8, 4, 768, 300, 512)
     t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
     rng = np.random.default_rng(21)
@@ -267,7 +269,7 @@ def test_fused_rope_attention_equals_separate_kernels():
         assert [s.position for s in sess] == [258, 44]
         out.append((np.array(lg), [s.kv() for s in sess]))
     (la, kva), (lb, kvb) = out
-    assert np.array_equal(la, lb)
+    assert relerr(la, lb) < 1e-5
     for (Ka, Va), (Kb, Vb), n in zip(kva, kvb, (258, 44)):
         assert np.array_equal(Ka[:, :n], Kb[:, :n]) and np.array_equal(Va[:, :n], Vb[:, :n])
 
