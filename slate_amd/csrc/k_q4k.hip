@@ -551,7 +551,10 @@ static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, i
     if (s_max < 1) s_max = 1;
     int R_out_v = (R_env == 1 || R_env == 2 || R_env == 4) ? R_env : 1, S_out_v = s_max;
     bool done = false;
-    for (int R = 4; R >= 1 && !done; R >>= 1) {
+    // R = 4 only when asked for: at the same wave target, two tiles per wave
+    // with half the splits (twice the blocks per wave) measured faster
+    // (gate+up 2x14336x4096 at 16 rows: 18.0 vs 19.8 us; LM head equal)
+    for (int R = R_env == 4 ? 4 : 2; R >= 1 && !done; R >>= 1) {
         if ((R_env == 1 || R_env == 2 || R_env == 4) && R != R_env) continue;
         int groups = 0;
         for (int i = 0; i < n; ++i) groups += (tiles[i] + R - 1) / R;
