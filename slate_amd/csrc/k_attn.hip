@@ -382,19 +382,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     }
 }
 
-// Decode work unit (one query token per sequence): (key chunk, token, kv
-// head), G query heads.  Each wave owns 64 keys of the 256-key chunk and
-// works through them without barriers:
-//   scores  8 lanes per key row (lane ls holds dims 32i + 4ls .. +3 of the
-//           row and of the G query slices; one load instruction of a wave
-//           covers 8 rows x 128 contiguous bytes), reduced over the 8 lanes
-//           by DPP; the wave's 8 x 8 scores per head stay in registers;
-//   softmax max and sum over the wave's keys;
-//   PV      the same lane owns the same key's V row slice, weighted by its
-//           own probability.
-// The waves then combine through LDS (log-sum-exp over the four wave
-// maxima) into the chunk partial (max m, sum l, unnormalised output), as
-// attn_block_kernel writes it.
 // Decode steps in which every sequence adds one token: the attention unit
 // also does what rope_kv_kernel does for its token and kv head, from the
 // QKV split partials (same expressions, same results).  part / nsplit /
@@ -464,6 +451,20 @@ __device__ __forceinline__ void attn_rope_prologue(const AttnRope& fr, int t, in
     }
 }
 
+// Decode work unit (one query token per sequence): (key chunk, token, kv
+// head), G query heads.  Each wave owns 64 keys of the 256-key chunk and
+// works through them without barriers:
+//   scores  8 lanes per key row (lane ls holds dims 32i + 4ls .. +3 of the
+//           row and of the G query slices; one load instruction of a wave
+//           covers 8 rows x 128 contiguous bytes), reduced over the 8 lanes
+//           by DPP; the wave's 8 x 8 scores per head stay in registers;
+//   softmax max and sum over the wave's keys;
+//   PV      the same lane owns the same key's V row slice, weighted by its
+//           own probability.
+// The waves then combine through LDS (log-sum-exp over the four wave
+// maxima) into the chunk partial (max m, sum l, unnormalised output), as
+// attn_block_kernel writes it.
+// With ROPE the unit first runs attn_rope_prologue (q from LDS afterwards).
 template <int HD, int G, typename KVT, bool ROPE>
 __device__ __forceinline__ void attn_dec_wave_body(
     const float* q, const KVT* Kp, const KVT* Vp, const int32_t* pairs, int Hq, int64_t head_stride, int nch_max,
