@@ -253,6 +253,75 @@ __device__ __forceinline__ float4 ld_kv4(const _Float16* p) {
     return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
 }
 
+// Decode steps in which every sequence adds one token: the attention unit
+// also does what rope_kv_kernel does for its token and kv head, from the
+// QKV split partials (same expressions, same results).  part / nsplit /
+// split_stride / qkv_ld: the partials; cs: the rotation table; rn: the
+// deferred RMSNorm factor (rn.ssq null: none); Kw / Vw: the caches written.
+struct AttnRope {
+    const float* part;
+    int nsplit;
+    int64_t split_stride;
+    int qkv_ld;
+    const float* cs;
+    RowNorm rn;
+    void *Kw, *Vw;
+};
+
+// The G query heads of kv head h for token t, rotated, into sq[G][HD]; when
+// `append`, the token's K and V rows of kv head h are written at position p
+// (kvb: the sequence's rows of kv head h).  Threads of one workgroup; the caller orders the
+// results with a barrier (and a fence for the rows).
+template <int HD, int G, typename KVT>
+__device__ __forceinline__ void attn_rope_prologue(const AttnRope& fr, int t, int h, int p, int64_t kvb, int Hq,
+                                                   int Hkv, bool append, float (*sq)[HD]) {
+#pragma clang fp contract(off)
+    constexpr int half = HD / 2;
+    const int tid = threadIdx.x;
+    const int ap = p < 0 ? -p : p;
+    const float sg = p < 0 ? -1.0f : 1.0f;
+    const float* pr = fr.part + (size_t)t * fr.qkv_ld;
+    const RowNorm& rn = fr.rn;
+    RmsPre rp;
+    if (rn.ssq) rp = row_rms_load(rn.ssq, t, rn.nblk);
+    float inv = 1.0f;
+    auto scale = [&](float v) { return rn.ssq ? v * inv : v; };
+    for (int idx = tid; idx < G * half; idx += ATT_THREADS) {
+        const int gi = idx / half, i = idx - gi * half;
+        const int c0 = (h * G + gi) * HD + i;
+        const Split1 pa = split_load1(pr + c0, fr.nsplit, fr.split_stride);
+        const Split1 pb = split_load1(pr + c0 + half, fr.nsplit, fr.split_stride);
+        const float c = fr.cs[((size_t)ap * half + i) * 2 + 0];
+        const float sn = sg * fr.cs[((size_t)ap * half + i) * 2 + 1];
+        if (rn.ssq) inv = row_rms_fin(rp, rn.ssq, t, rn.nblk, rn.D, rn.eps);
+        const float a = scale(split_fin1(pa, pr + c0, fr.nsplit, fr.split_stride));
+        const float b = scale(split_fin1(pb, pr + c0 + half, fr.nsplit, fr.split_stride));
+        sq[gi][i] = a * c - b * sn;
+        sq[gi][i + half] = a * sn + b * c;
+    }
+    if (!append) return;
+    KVT* Kw = (KVT*)fr.Kw;
+    KVT* Vw = (KVT*)fr.Vw;
+    const int D = Hq * HD, kvd = Hkv * HD;
+    for (int i = tid; i < half; i += ATT_THREADS) {
+        const int ck = D + h * HD + i, cv = D + kvd + h * HD + i;
+        const Split1 pa = split_load1(pr + ck, fr.nsplit, fr.split_stride);
+        const Split1 pb = split_load1(pr + ck + half, fr.nsplit, fr.split_stride);
+        const Split1 pv0 = split_load1(pr + cv, fr.nsplit, fr.split_stride);
+        const Split1 pv1 = split_load1(pr + cv + half, fr.nsplit, fr.split_stride);
+        const float c = fr.cs[((size_t)ap * half + i) * 2 + 0];
+        const float sn = sg * fr.cs[((size_t)ap * half + i) * 2 + 1];
+        const int64_t base = kvb + (int64_t)p * HD;
+        if (rn.ssq) inv = row_rms_fin(rp, rn.ssq, t, rn.nblk, rn.D, rn.eps);
+        const float a = scale(split_fin1(pa, pr + ck, fr.nsplit, fr.split_stride));
+        const float b = scale(split_fin1(pb, pr + ck + half, fr.nsplit, fr.split_stride));
+        Kw[base + i] = (KVT)(a * c - b * sn);
+        Kw[base + i + half] = (KVT)(a * sn + b * c);
+        Vw[base + i] = (KVT)scale(split_fin1(pv0, pr + cv, fr.nsplit, fr.split_stride));
+        Vw[base + i + half] = (KVT)scale(split_fin1(pv1, pr + cv + half, fr.nsplit, fr.split_stride));
+    }
+}
+
 // Decode work unit (one query token per sequence): (key chunk, token, kv
 // head), G query heads.  Every K and V row of the chunk is read once, whole
 // and coalesced:
@@ -264,17 +333,17 @@ __device__ __forceinline__ float4 ld_kv4(const _Float16* p) {
 //   PV      HD/4 lanes per V row (64/(HD/4) rows per wave instruction), the
 //           probabilities broadcast from LDS, reduced over lanes and waves.
 // Partials (chunk max m, sum l, unnormalised output) as attn_block_kernel.
-template <int HD, int G, typename KVT>
-__global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
-    const float* __restrict__ q, const KVT* __restrict__ Kp, const KVT* __restrict__ Vp,
-    const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
-    const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
-    float* __restrict__ pml, const int32_t* __restrict__ pairs) {
+// With ROPE the unit first runs attn_rope_prologue (q from LDS afterwards).
+template <int HD, int G, typename KVT, bool ROPE>
+__device__ __forceinline__ void attn_dec_body(const float* q, const KVT* Kp, const KVT* Vp, const int32_t* pairs,
+                                              int Hq, int64_t head_stride, int nch_max, float* po, float* pml,
+                                              const AttnRope& fr, int Hkv) {
     constexpr int NV = HD / 32;
     constexpr int LPR = HD / 4;
     constexpr int KPI = 64 / LPR;
     __shared__ float sp[G][ATT_CHUNK];
     __shared__ float4 sred[4][G][LPR];
+    __shared__ float s_q[ROPE ? G : 1][ROPE ? HD : 1];
     // work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
     // wrote; the units past its count are the grid's empty tail
     const AttnUnit un = attn_unit(pairs, blockIdx.x);
@@ -288,6 +357,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     const int lg = lane >> 3, ls = lane & 7;
     const float scale = 1.0f / sqrtf((float)HD);
     const int64_t base = un.kvb + (int64_t)h * head_stride + (int64_t)k0 * HD;
+    if constexpr (ROPE) {
+        // the unit of the chunk holding key p appends the token's K and V
+        // rows; the fence and barrier make them visible to the key loads
+        const bool append = p - k0 < ATT_CHUNK;
+        attn_rope_prologue<HD, G, KVT>(fr, t, h, p, un.kvb + (int64_t)h * head_stride, Hq, Hkv, append, s_q);
+        if (append) __threadfence_block();
+        __syncthreads();
+    }
     const KVT* Kh = Kp + base;
     const KVT* Vh = Vp + base;
     const float* qt = q + (size_t)t * Hq * HD + (size_t)h * G * HD;
@@ -295,7 +372,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
 #pragma unroll
     for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-        for (int i = 0; i < NV; ++i) qv[gi][i] = *(const float4*)(qt + gi * HD + 32 * i + 4 * ls);
+        for (int i = 0; i < NV; ++i)
+            qv[gi][i] = ROPE ? *(const float4*)(&s_q[gi][32 * i + 4 * ls])
+                             : *(const float4*)(qt + gi * HD + 32 * i + 4 * ls);
 
     // ---- scores
 #pragma unroll 2
@@ -382,73 +461,23 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
     }
 }
 
-// Decode steps in which every sequence adds one token: the attention unit
-// also does what rope_kv_kernel does for its token and kv head, from the
-// QKV split partials (same expressions, same results).  part / nsplit /
-// split_stride / qkv_ld: the partials; cs: the rotation table; rn: the
-// deferred RMSNorm factor (rn.ssq null: none); Kw / Vw: the caches written.
-struct AttnRope {
-    const float* part;
-    int nsplit;
-    int64_t split_stride;
-    int qkv_ld;
-    const float* cs;
-    RowNorm rn;
-    void *Kw, *Vw;
-};
-
-// The G query heads of kv head h for token t, rotated, into sq[G][HD]; when
-// `append`, the token's K and V rows of kv head h are written at position p
-// (kvb: the sequence's rows of kv head h).  Threads of one workgroup; the caller orders the
-// results with a barrier (and a fence for the rows).
 template <int HD, int G, typename KVT>
-__device__ __forceinline__ void attn_rope_prologue(const AttnRope& fr, int t, int h, int p, int64_t kvb, int Hq,
-                                                   int Hkv, bool append, float (*sq)[HD]) {
-#pragma clang fp contract(off)
-    constexpr int half = HD / 2;
-    const int tid = threadIdx.x;
-    const int ap = p < 0 ? -p : p;
-    const float sg = p < 0 ? -1.0f : 1.0f;
-    const float* pr = fr.part + (size_t)t * fr.qkv_ld;
-    const RowNorm& rn = fr.rn;
-    RmsPre rp;
-    if (rn.ssq) rp = row_rms_load(rn.ssq, t, rn.nblk);
-    float inv = 1.0f;
-    auto scale = [&](float v) { return rn.ssq ? v * inv : v; };
-    for (int idx = tid; idx < G * half; idx += ATT_THREADS) {
-        const int gi = idx / half, i = idx - gi * half;
-        const int c0 = (h * G + gi) * HD + i;
-        const Split1 pa = split_load1(pr + c0, fr.nsplit, fr.split_stride);
-        const Split1 pb = split_load1(pr + c0 + half, fr.nsplit, fr.split_stride);
-        const float c = fr.cs[((size_t)ap * half + i) * 2 + 0];
-        const float sn = sg * fr.cs[((size_t)ap * half + i) * 2 + 1];
-        if (rn.ssq) inv = row_rms_fin(rp, rn.ssq, t, rn.nblk, rn.D, rn.eps);
-        const float a = scale(split_fin1(pa, pr + c0, fr.nsplit, fr.split_stride));
-        const float b = scale(split_fin1(pb, pr + c0 + half, fr.nsplit, fr.split_stride));
-        sq[gi][i] = a * c - b * sn;
-        sq[gi][i + half] = a * sn + b * c;
-    }
-    if (!append) return;
-    KVT* Kw = (KVT*)fr.Kw;
-    KVT* Vw = (KVT*)fr.Vw;
-    const int D = Hq * HD, kvd = Hkv * HD;
-    for (int i = tid; i < half; i += ATT_THREADS) {
-        const int ck = D + h * HD + i, cv = D + kvd + h * HD + i;
-        const Split1 pa = split_load1(pr + ck, fr.nsplit, fr.split_stride);
-        const Split1 pb = split_load1(pr + ck + half, fr.nsplit, fr.split_stride);
-        const Split1 pv0 = split_load1(pr + cv, fr.nsplit, fr.split_stride);
-        const Split1 pv1 = split_load1(pr + cv + half, fr.nsplit, fr.split_stride);
-        const float c = fr.cs[((size_t)ap * half + i) * 2 + 0];
-        const float sn = sg * fr.cs[((size_t)ap * half + i) * 2 + 1];
-        const int64_t base = kvb + (int64_t)p * HD;
-        if (rn.ssq) inv = row_rms_fin(rp, rn.ssq, t, rn.nblk, rn.D, rn.eps);
-        const float a = scale(split_fin1(pa, pr + ck, fr.nsplit, fr.split_stride));
-        const float b = scale(split_fin1(pb, pr + ck + half, fr.nsplit, fr.split_stride));
-        Kw[base + i] = (KVT)(a * c - b * sn);
-        Kw[base + i + half] = (KVT)(a * sn + b * c);
-        Vw[base + i] = (KVT)scale(split_fin1(pv0, pr + cv, fr.nsplit, fr.split_stride));
-        Vw[base + i + half] = (KVT)scale(split_fin1(pv1, pr + cv + half, fr.nsplit, fr.split_stride));
-    }
+__global__ __launch_bounds__(ATT_THREADS) void attn_dec_kernel(
+    const float* __restrict__ q, const KVT* __restrict__ Kp, const KVT* __restrict__ Vp,
+    const int32_t* __restrict__ dec_t0, const int32_t* __restrict__ tok2seq, const int32_t* __restrict__ tok_pos,
+    const int64_t* __restrict__ kv_base, int Hq, int64_t head_stride, int nch_max, float* __restrict__ po,
+    float* __restrict__ pml, const int32_t* __restrict__ pairs) {
+    attn_dec_body<HD, G, KVT, false>(q, Kp, Vp, pairs, Hq, head_stride, nch_max, po, pml, AttnRope{}, 0);
+}
+
+// The phased unit with the rotation and KV append of the step's tokens (one
+// token per sequence); Kp / Vp are not __restrict__ (rows written through
+// fr.Kw / fr.Vw are read back).
+template <int HD, int G, typename KVT>
+__global__ __launch_bounds__(ATT_THREADS) void attn_dec_phased_rope_kernel(
+    const KVT* Kp, const KVT* Vp, int Hq, int Hkv, int64_t head_stride, int nch_max, float* __restrict__ po,
+    float* __restrict__ pml, const int32_t* __restrict__ pairs, AttnRope fr) {
+    attn_dec_body<HD, G, KVT, true>(nullptr, Kp, Vp, pairs, Hq, head_stride, nch_max, po, pml, fr, Hkv);
 }
 
 // Decode work unit (one query token per sequence): (key chunk, token, kv
@@ -905,30 +934,39 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
     return 0;
 }
 
-// SLATE_HIP_ATTN_ROPE=0 keeps rope_kv_kernel separate in decode steps.
-static bool rope_fused() {
-    static const bool on = getenv("SLATE_HIP_ATTN_ROPE") == nullptr || atoi(getenv("SLATE_HIP_ATTN_ROPE")) != 0;
-    return on;
+// SLATE_HIP_ATTN_ROPE: 0 keeps rope_kv_kernel separate in decode steps;
+// 1 (default) fuses it into the wave kernel where that kernel runs the
+// shape (G * HD <= 512, <= 64 tokens) and into the phased kernel elsewhere;
+// 2 always into the phased kernel.  The two fused kernels measured equal
+// on the 8B bench (3781 tok/s each).
+static int rope_fused() {
+    static const int k = getenv("SLATE_HIP_ATTN_ROPE") ? atoi(getenv("SLATE_HIP_ATTN_ROPE")) : 1;
+    return k == 0 || k == 2 ? k : 1;
 }
 
 template <int HD, int G, typename KVT>
-static void launch_rope_t(dim3 grid, hipStream_t s, hipEvent_t ev0, const void* Kp, const void* Vp, int Hq, int Hkv,
-                          int64_t head_stride, int nch_max, float* po, float* pml, const int32_t* pairs,
-                          const AttnRope& fr) {
-    SH_LAUNCH(ev0, nullptr, (attn_dec_rope_kernel<HD, G, KVT>), grid, dim3(ATT_THREADS), 0, s, (const KVT*)Kp,
-              (const KVT*)Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
+static void launch_rope_t(bool wave, dim3 grid, hipStream_t s, hipEvent_t ev0, const void* Kp, const void* Vp,
+                          int Hq, int Hkv, int64_t head_stride, int nch_max, float* po, float* pml,
+                          const int32_t* pairs, const AttnRope& fr) {
+    if constexpr (G * HD <= 512) {
+        if (wave) {
+            SH_LAUNCH(ev0, nullptr, (attn_dec_rope_kernel<HD, G, KVT>), grid, dim3(ATT_THREADS), 0, s, (const KVT*)Kp,
+                      (const KVT*)Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
+            return;
+        }
+    }
+    SH_LAUNCH(ev0, nullptr, (attn_dec_phased_rope_kernel<HD, G, KVT>), grid, dim3(ATT_THREADS), 0, s,
+              (const KVT*)Kp, (const KVT*)Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
 }
 
 template <int HD, int G>
 static int launch_rope_g(bool f16, dim3 grid, hipStream_t s, hipEvent_t ev0, const void* Kp, const void* Vp, int Hq,
                          int Hkv, int64_t head_stride, int nch_max, float* po, float* pml, const int32_t* pairs,
                          const AttnRope& fr) {
-    if constexpr (G * HD <= 512) {
-        if (f16) launch_rope_t<HD, G, _Float16>(grid, s, ev0, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
-        else launch_rope_t<HD, G, float>(grid, s, ev0, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
-        return 0;
-    }
-    return 1;
+    const bool wave = rope_fused() == 1 && wave_kernel() && G * HD <= 512 && (int)grid.x / nch_max <= ATT_WAVE_MAX_TOKENS;
+    if (f16) launch_rope_t<HD, G, _Float16>(wave, grid, s, ev0, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
+    else launch_rope_t<HD, G, float>(wave, grid, s, ev0, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml, pairs, fr);
+    return 0;
 }
 
 template <int HD>
@@ -949,7 +987,7 @@ int launch_attention_rope(float* out, void* Kp, void* Vp, const float* part, int
                           int Hkv, int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
                           hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool kv_f16) {
     if (T <= 0) return 0;
-    if (!rope_fused() || !wave_kernel() || T > ATT_WAVE_MAX_TOKENS || Hkv <= 0 || Hq % Hkv != 0 ||
+    if (rope_fused() == 0 || Hkv <= 0 || Hq % Hkv != 0 ||
         !(HD == 32 || HD == 64 || HD == 128))
         return 1;
     if (act && ((Hq * HD) % 256 || act->K != Hq * HD)) return 1;
