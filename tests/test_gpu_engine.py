@@ -237,6 +237,46 @@ def test_q4k_decode_steps_match_oracle(orc):
             tok = int(np.argmax(steps[k][i]))
 
 
+def run_fused_and_separate(shape, prompts, extra):
+    """The same tokens through single-token steps (RoPE/append fused into
+    decode attention) and through one step of several tokens per sequence
+    (separate kernels): final logits and each session's K/V cache."""
+    t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
+    out = []
+    n_ex = len(extra[0])
+    for fused in (True, False):
+        m = slate_amd.Llama.from_tensors(shape, t, max_slots=len(prompts), max_tokens=512)
+        sess = [m.session() for _ in prompts]
+        rc, _, _ = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts), want_logits=False)
+        assert rc == 0
+        if fused:
+            for k in range(n_ex):
+                rc, lg, _ = m.step(sess, [1] * len(prompts), np.array([e[k] for e in extra], np.int32))
+                assert rc == 0
+        else:
+            rc, lg, _ = m.step(sess, [n_ex] * len(prompts), np.concatenate(extra))
+            assert rc == 0
+        assert [s.position for s in sess] == [len(p) + n_ex for p in prompts]
+        out.append((np.array(lg), [s.kv() for s in sess]))
+    return out
+
+
+def test_fused_rope_phased_attention_equals_separate_kernels():
+    """As below for a head group too wide for the wave kernel (8 query heads of
+    128 per kv head, as the 70B shape): the fused path runs in the phased
+    kernel, the separate path in the same kernel without the prologue; K/V
+    caches bit-identical, logits within 1e-5."""
+    shape = LlamaShape(2, 2048, 16, 2, 768, 300, 512)
+    rng = np.random.default_rng(22)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (253, 30)]
+    extra = [rng.integers(0, shape.vocab, 4).astype(np.int32) for _ in prompts]
+    (la, kva), (lb, kvb) = run_fused_and_separate(shape, prompts, extra)
+    assert relerr(la, lb) < 1e-5
+    for (Ka, Va), (Kb, Vb), p in zip(kva, kvb, prompts):
+        n = len(p) + 4
+        assert np.array_equal(Ka[:, :n], Kb[:, :n]) and np.array_equal(Va[:, :n], Vb[:, :n])
+
+
 def test_fused_rope_attention_equals_separate_kernels():
     """Steps in which every sequence adds one token rotate q/k and append K/V
     inside the decode attention kernel; a step adding several tokens of a
@@ -249,26 +289,10 @@ def test_fused_rope_attention_equals_separate_kernels():
     final logits agree within 1e-5: single-token steps also defer the final
     RMSNorm factor to the argmax, the four-token step normalises the rows."""
     shape = LlamaShape(2, 512, 8, 4, 768, 300, 512)
-    t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
     rng = np.random.default_rng(21)
     prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (254, 40)]
     extra = [rng.integers(0, shape.vocab, 4).astype(np.int32) for _ in prompts]
-    out = []
-    for fused in (True, False):
-        m = slate_amd.Llama.from_tensors(shape, t, max_slots=2, max_tokens=512)
-        sess = [m.session() for _ in prompts]
-        rc, _, _ = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts), want_logits=False)
-        assert rc == 0
-        if fused:
-            for k in range(4):
-                rc, lg, _ = m.step(sess, [1, 1], np.array([e[k] for e in extra], np.int32))
-                assert rc == 0
-        else:
-            rc, lg, _ = m.step(sess, [4, 4], np.concatenate(extra))
-            assert rc == 0
-        assert [s.position for s in sess] == [258, 44]
-        out.append((np.array(lg), [s.kv() for s in sess]))
-    (la, kva), (lb, kvb) = out
+    (la, kva), (lb, kvb) = run_fused_and_separate(shape, prompts, extra)
     assert relerr(la, lb) < 1e-5
     for (Ka, Va), (Kb, Vb), n in zip(kva, kvb, (258, 44)):
         assert np.array_equal(Ka[:, :n], Kb[:, :n]) and np.array_equal(Va[:, :n], Vb[:, :n])
