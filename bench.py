@@ -143,8 +143,8 @@ def main():
         print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 5}))
         return 0
     if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU sharding is described "
-                                   "in DESIGN.md and not executed", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this benchmark runs on one GPU; sequence-level data parallelism over "
+                                   "several GPUs is designed but not executed", "n_gpus": args.gpus}))
         return 2
     if args.ops:
         print(json.dumps(run_ops(args.seed)), flush=True)
