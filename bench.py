@@ -29,7 +29,9 @@ B = 64 sequences, 32 q / 8 kv heads, head_dim 128, lengths
 clip(round(exp(N(ln 1024, 1))), 16, 16384).  Each figure is the device time
 of a captured graph of many calls (no host launch gaps) divided by the calls.
 --copy-calibration instead runs a plain device copy of known size (for
-scaling the PMC byte counters).
+scaling the PMC byte counters).  --shape 70b runs the same workload with the
+70B layer shapes (80 layers, d_model 8192, 64 Q / 8 KV heads, SwiGLU 28672;
+no CPU baseline, no traffic figure: the PMC summary is of the 8B shape).
 """
 import argparse
 import json
@@ -125,7 +127,9 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--batch", type=int, default=16)
-    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=None, help="layers (default: the shape's own)")
+    ap.add_argument("--shape", choices=("8b", "70b"), default="8b",
+                    help="model shape: 8b (the headline line) or 70b (same workload, 70B layer shapes)")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -156,13 +160,21 @@ def main():
 
     import slate_amd
     from slate_amd.synth import LlamaShape
-    shape = LlamaShape(n_layers=args.layers, d_model=4096, n_heads=32, n_kv_heads=8, ffn=14336,
-                       vocab=128256, max_seq=2304)
+    big = args.shape == "70b"
+    if args.layers is None:
+        args.layers = 80 if big else 32
+    if big:
+        shape = LlamaShape(n_layers=args.layers, d_model=8192, n_heads=64, n_kv_heads=8, ffn=28672,
+                           vocab=128256, max_seq=2304)
+        args.no_cpu = True    # the reference's C decode step needs ~13 s per token per core at this shape
+    else:
+        shape = LlamaShape(n_layers=args.layers, d_model=4096, n_heads=32, n_kv_heads=8, ffn=14336,
+                           vocab=128256, max_seq=2304)
     max_tokens = 4096
     t0 = time.perf_counter()
     m = slate_amd.Llama.synthetic(shape, seed=args.seed, quant=18, max_slots=args.batch + 1,
                                   max_tokens=max_tokens)
-    log(f"synthetic 8B-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
+    log(f"synthetic {args.shape.upper()}-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
     wl = Workload(m, shape, args.batch, args.seed + 1, max_tokens)
     t0 = time.perf_counter()
     wl.prefill_all()
@@ -212,7 +224,8 @@ def main():
     kname = "q4k_dec_kernel" if dom == "q4k_mm" else "attn_dec_kernel+attn_merge_kernel"
     roofline = {"bound": "hbm", "kernel": kname,
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kname),
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": None if big else measured_traffic(kname),   # the PMC summary is of the 8B shape
                 "launches": n, "avg_launch_us": round(ms * 1e3 / max(n, 1), 2),
                 "algorithmic_bytes_per_launch": round(by / max(n, 1))}
     other = "attention" if dom == "q4k_mm" else "q4k_mm"
@@ -220,12 +233,14 @@ def main():
     step_ms, _, step_n = raw["step"]
     pf_ms, pf_by, pf_n = raw["q4k_mm_pf"]
     result = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC.replace("8B-shape", "70B-shape") if big else METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "LLaMA-3-8B-shaped Q4_K decode, ragged continuous batching B=16 "
+        "config": {"workload": ("LLaMA-70B-shaped" if big else "LLaMA-3-8B-shaped") +
+                               f" Q4_K decode, ragged continuous batching B={args.batch} "
                                "(contexts U[128,2048], stop U[32,256], arrivals with U[64,512]-token prompts)",
-                   "layers": args.layers, "d_model": 4096, "heads": "32q/8kv", "ffn": 14336, "vocab": 128256,
+                   "layers": args.layers, "d_model": shape.d_model,
+                   "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "q4_k", "kv_cache": "f16" if lib.slate_hip_llama_kv_f16(m.h) == 1 else "f32",
                    "batch": args.batch,
                    "mixed_prefill_steps": mixed_steps, "arrivals": wl.arrivals - arrivals0,
