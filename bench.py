@@ -475,7 +475,19 @@ def cpu_baseline_from(m, shape, snap, gpu, budget_s=40.0):
                 sample=f"slate_llama_decode_step (slate's C, built from its sources, single thread as wired) "
                        f"on the benchmark's weights and KV state: one decode step of {n_tok} sequences, "
                        f"{t_cpu:.1f} s",
-                host_cores_available=os.cpu_count(), logits_max_rel_vs_gpu=worst)
+                host_cores_available=os.cpu_count(), host_cpu=cpu_model(), logits_max_rel_vs_gpu=worst)
+
+
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 if __name__ == "__main__":
