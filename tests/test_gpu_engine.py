@@ -261,6 +261,31 @@ def run_fused_and_separate(shape, prompts, extra):
     return out
 
 
+def test_fused_rope_attention_first_token_of_a_session(orc):
+    """A fresh session's first token in a step where every sequence adds one
+    token: the fused decode attention appends K/V at position 0 and attends
+    that key alone; logits of both sequences against the oracle, and the
+    following steps too."""
+    t = make_llama(FUSE, 4321, quant="q4k", output_quant="q4k")
+    om = OracleModel(orc, FUSE, t)
+    m = slate_amd.Llama.from_tensors(FUSE, t, max_slots=2, max_tokens=32)
+    a, b = m.session(), m.session()
+    oa, ob = om.session(), om.session()
+    rng = np.random.default_rng(23)
+    pa = rng.integers(0, FUSE.vocab, 7).astype(np.int32)
+    rc, _, _ = m.step([a], [len(pa)], pa, want_logits=False)
+    assert rc == 0
+    oa.prefill(pa)
+    toks = rng.integers(0, FUSE.vocab, (3, 2)).astype(np.int32)
+    for k in range(3):
+        rc, lg, _ = m.step([a, b], [1, 1], toks[k])
+        assert rc == 0
+        _, wa = oa.decode(int(toks[k][0]))
+        _, wb = (ob.prefill(toks[k][1:2]) if k == 0 else ob.decode(int(toks[k][1])))
+        assert relerr(lg[0], wa) < TOL and relerr(lg[1], wb) < TOL, k
+    assert b.position == 3 and a.position == 10
+
+
 def test_fused_rope_phased_attention_equals_separate_kernels():
     """As below for a head group too wide for the wave kernel (8 query heads of
     128 per kv head, as the 70B shape): the fused path runs in the phased
