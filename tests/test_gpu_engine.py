@@ -286,6 +286,38 @@ def test_fused_rope_attention_first_token_of_a_session(orc):
     assert b.position == 3 and a.position == 10
 
 
+@pytest.mark.parametrize("d_model,n_heads,n_kv_heads", [(512, 4, 4), (512, 8, 1), (256, 8, 8)])
+def test_fused_rope_attention_head_groups(orc, d_model, n_heads, n_kv_heads):
+    """The fused decode attention at more head groups than the model tests
+    reach: G = 1 with head_dim 128, G = 8 with head_dim 64 (G * HD = 512, the
+    wave kernel's limit), G = 1 with head_dim 32; a prompt step, then decode
+    steps of two sequences, every step against the oracle."""
+    shape = LlamaShape(2, d_model, n_heads, n_kv_heads, 512, 300, 320)
+    t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(24)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (260, 9)]
+    m = slate_amd.Llama.from_tensors(shape, t, max_slots=2, max_tokens=320)
+    sess = [m.session() for _ in prompts]
+    rc, lg, nxt = m.step(sess, [len(p) for p in prompts], np.concatenate(prompts))
+    assert rc == 0
+    steps, toks = [lg], np.asarray(nxt, np.int32)
+    for _ in range(4):
+        rc, lg, nxt = m.step(sess, [1, 1], toks)
+        assert rc == 0
+        steps.append(lg)
+        toks = np.asarray(nxt, np.int32)
+    om = OracleModel(orc, shape, t)
+    for i, p in enumerate(prompts):
+        o = om.session()
+        rc, want = o.prefill(p)
+        assert rc == 0 and relerr(steps[0][i], want) < TOL
+        tok = int(np.argmax(steps[0][i]))
+        for k in range(1, len(steps)):
+            rc, want = o.decode(tok)
+            assert rc == 0 and relerr(steps[k][i], want) < TOL, (i, k)
+            tok = int(np.argmax(steps[k][i]))
+
+
 def test_fused_rope_phased_attention_equals_separate_kernels():
     """As below for a head group too wide for the wave kernel (8 query heads of
     128 per kv head, as the 70B shape): the fused path runs in the phased
