@@ -36,10 +36,23 @@
 extern "C" {
 #endif
 
-/* ---- include/slate/backend.h:41-99, reproduced member for member so that
- * this header and slate's can be included in either order. ---------------- */
-#ifndef SLATE_BACKEND_H
-#define SLATE_BACKEND_H
+/* ---- slate_backend_t (include/slate/backend.h:41-99) ----------------------
+ * When slate's own header is visible -- already included, or reachable as
+ * "slate/backend.h" on the include path -- it is used as is, factories
+ * (backend.h:104-110) included.  Otherwise the same struct is declared here,
+ * member for member, under this header's own guard; slate's guard
+ * SLATE_BACKEND_H is never defined here, so a translation unit that later
+ * includes slate/backend.h by another path gets a loud redefinition error
+ * rather than a silently skipped header.  In a TU that uses both headers,
+ * put slate's include/ directory on the include path (or include
+ * slate/backend.h first). */
+#if !defined(SLATE_BACKEND_H) && defined(__has_include)
+#if __has_include("slate/backend.h")
+#include "slate/backend.h"
+#endif
+#endif
+#if !defined(SLATE_BACKEND_H) && !defined(SLATE_HIP_BACKEND_T_DECLARED)
+#define SLATE_HIP_BACKEND_T_DECLARED 1
 typedef struct slate_backend {
     const char* name;
     void* (*alloc)(size_t bytes);

@@ -453,6 +453,21 @@ void orc_session_kv(const orc_session* s, float* K_out, float* V_out) {
     memcpy(V_out, s->V, n * sizeof(float));
 }
 
+/* Load a KV state (K/V [n_layers, max_seq, kv_dim], the layout
+ * orc_session_kv returns) and a position, so that decode steps can be
+ * checked from a context that another implementation built.  Test
+ * infrastructure, like ref_session_set_state for the compiled reference. */
+int orc_session_set_state(orc_session* s, const float* K, const float* V, int pos) {
+    if (!s || !K || !V) return -1;
+    const orc_llama_cfg* c = &s->m->cfg;
+    if (pos < 0 || pos > c->max_seq) return -1;
+    size_t n = (size_t)c->n_layers * c->max_seq * c->n_kv_heads * c->head_dim;
+    memcpy(s->K, K, n * sizeof(float));
+    memcpy(s->V, V, n * sizeof(float));
+    s->pos = pos;
+    return 0;
+}
+
 /* llama_infer.c:43-51 -- dtype 18 (Q4_K) takes the Q4_K matvec and f32 the
  * f32 one.  Dtype 16 (Q8_0) is where this restatement departs on purpose:
  * the reference reads a Q8_0 tensor's bytes as f32 (its dispatch knows only

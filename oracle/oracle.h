@@ -120,6 +120,7 @@ int          orc_decode_step(orc_session* s, int32_t token, float* logits);     
 int          orc_prefill(orc_session* s, const int32_t* toks, int n, float* logits); /* llama_infer.c:262-272 */
 /* Copy a session's KV cache out ([n_layers, max_seq, kv_dim] each). */
 void         orc_session_kv(const orc_session* s, float* K_out, float* V_out);
+int          orc_session_set_state(orc_session* s, const float* K, const float* V, int pos);
 
 #ifdef __cplusplus
 }

@@ -102,6 +102,7 @@ class Oracle:
         _sig(L, "orc_decode_step", C.c_int, vp, C.c_int32, f32p)
         _sig(L, "orc_prefill", C.c_int, vp, i32p, C.c_int, f32p)
         _sig(L, "orc_session_kv", None, vp, f32p, f32p)
+        _sig(L, "orc_session_set_state", C.c_int, vp, f32p, f32p, C.c_int)
 
     # -- numpy conveniences ------------------------------------------------
     def dequant_q4k(self, raw, n):
@@ -196,6 +197,10 @@ class OracleSession:
         rc = self.m.orc.lib.orc_decode_step(self.h, int(tok), fp(lg))
         return rc, lg
 
+    def set_state(self, K, V, pos):
+        return self.m.orc.lib.orc_session_set_state(self.h, fp(np.ascontiguousarray(K, np.float32)),
+                                                    fp(np.ascontiguousarray(V, np.float32)), pos)
+
     def kv(self):
         s = self.m.shape
         n = s.n_layers * s.max_seq * s.kv_dim
@@ -247,6 +252,8 @@ class Ref:
         _sig(L, "slate_llama_decode_step", C.c_int, vp, C.c_int32, f32p)
         _sig(L, "ref_session_set_state", C.c_int, vp, f32p, f32p, C.c_int)
         _sig(L, "ref_session_get_kv", C.c_int, vp, f32p, f32p)
+        _sig(L, "ref_decode_sessions_parallel", None, C.POINTER(vp), i32p, C.c_int, f32p, i32p)
+        _sig(L, "ref_pool_threads", C.c_int)
         be = L.slate_backend_cpu().contents
         self.cpu = be
         T = C.CFUNCTYPE

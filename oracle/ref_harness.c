@@ -6,6 +6,7 @@
  * in oracle/_ref/ and is never shipped or linked by the product.
  */
 #include "src/loader/llama_infer.c"
+#include "slate/runtime.h"
 
 /* llama_infer.c:77-92 */
 void ref_rope_inplace_row(float* row, int n_heads, int head_dim, int position,
@@ -44,3 +45,32 @@ int ref_session_get_kv(const slate_llama_session_t* s, float* K, float* V) {
     memcpy(V, s->V_cache, n * sizeof(float));
     return 0;
 }
+
+/* Harness-level parallelism, not wired in slate's LLaMA path (which decodes
+ * one session at a time on one thread): one decode step for each of n
+ * sessions, the sessions spread over slate's own global threadpool
+ * (slate_threadpool_parallel_for, threadpool.c:122-142; its size comes from
+ * SLATE_NUM_THREADS or the online CPU count, pool_global.c:18-25).  Logits
+ * of session i go to logits[i * vocab ..]; rc[i] is its return code. */
+typedef struct {
+    slate_llama_session_t** s;
+    const int32_t* tok;
+    float* logits;
+    int vocab;
+    int* rc;
+} ref_par_job;
+
+static void ref_par_task(int i, int n, void* u) {
+    (void)n;
+    ref_par_job* j = (ref_par_job*)u;
+    j->rc[i] = slate_llama_decode_step(j->s[i], j->tok[i], j->logits + (size_t)i * j->vocab);
+}
+
+void ref_decode_sessions_parallel(slate_llama_session_t** s, const int32_t* tok, int n, float* logits,
+                                  int* rc) {
+    if (!s || n <= 0) return;
+    ref_par_job j = {s, tok, logits, slate_llama_config(s[0]->model)->vocab, rc};
+    slate_threadpool_parallel_for(slate_global_pool(), n, ref_par_task, &j);
+}
+
+int ref_pool_threads(void) { return slate_threadpool_num_threads(slate_global_pool()); }

@@ -10,6 +10,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -86,6 +87,37 @@ static bool ensure() {
 
 bool device_ok() { return ensure(); }
 hipStream_t stream() { return ensure() ? g_stream : nullptr; }
+
+static Knobs g_knobs;
+static std::once_flag g_knobs_once;
+
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : dflt;
+}
+
+void reload_knobs() {
+    Knobs k;
+    k.attn_wave = env_int("SLATE_HIP_ATTN_WAVE", 1) != 0;
+    k.attn_rope = env_int("SLATE_HIP_ATTN_ROPE", 1);
+    if (k.attn_rope != 0 && k.attn_rope != 2) k.attn_rope = 1;
+    k.q4k_w = env_int("SLATE_HIP_Q4K_W", 8) == 4 ? 4 : 8;
+    k.q4k_r = env_int("SLATE_HIP_Q4K_R", 0);
+    if (k.q4k_r != 1 && k.q4k_r != 2 && k.q4k_r != 4) k.q4k_r = 0;
+    k.q4k_s = std::max(0, env_int("SLATE_HIP_Q4K_S", 0));
+    k.q4k_wgs = std::max(1, env_int("SLATE_HIP_Q4K_WGS", 448));
+    k.q4k_pf_s = std::max(0, env_int("SLATE_HIP_Q4K_PF_S", 0));
+    k.q8_r = env_int("SLATE_HIP_Q8_R", 0);
+    if (k.q8_r != 1 && k.q8_r != 2 && k.q8_r != 4) k.q8_r = 0;
+    k.q8_s = std::max(0, env_int("SLATE_HIP_Q8_S", 0));
+    k.q8_wgs = std::max(1, env_int("SLATE_HIP_Q8_WGS", 448));
+    g_knobs = k;
+}
+
+const Knobs& knobs() {
+    std::call_once(g_knobs_once, reload_knobs);
+    return g_knobs;
+}
 
 // Serialises multi-kernel entry sequences that share scratch buffers.
 std::mutex g_enqueue_mu;
@@ -218,6 +250,10 @@ static int matmul_q4k_common(float* Y, const void* A, const float* X, int B, int
     SH_REQUIRE(Y && A && X && B > 0 && M > 0 && K > 0, "matmul_q4k: bad arguments");
     SH_REQUIRE(K % QK == 0, "matmul_q4k: K=%d is not a multiple of 256", K);
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    Q4kTarget t{A, M, 0};
+    // a few rows: one GEMV kernel straight into Y (no operand, no partials)
+    if (B <= GEMV_MAX_ROWS && ((uintptr_t)X & 15) == 0)
+        return launch_q4k_gemv(&t, 1, tiled, X, K, B, K, Y, M, g_stream);
     Act16 a;
     if (make_act16(a, B, K, 0)) return -2;
     int rc = launch_act16_from_f32(a, X, K, g_stream);
@@ -225,7 +261,6 @@ static int matmul_q4k_common(float* Y, const void* A, const float* X, int B, int
     const int max_splits = 32;
     float* part = (float*)scratch(1, (size_t)max_splits * a.rows_pad * M * sizeof(float));
     if (!part) return -2;
-    Q4kTarget t{A, M, 0};
     int S = 1;
     rc = launch_q4k(&t, 1, tiled, a, part, (int64_t)M, (int64_t)a.rows_pad * M, max_splits, &S, g_stream);
     if (rc) return rc;
@@ -239,6 +274,7 @@ int slate_hip_matmul_q4k(float* Y, const void* A, const float* X, int B, int M, 
 int slate_hip_matmul_q4k_tiled(float* Y, const void* A, const float* X, int B, int M, int K) {
     return matmul_q4k_common(Y, A, X, B, M, K, true);
 }
+
 
 int64_t slate_hip_q4k_tiled_bytes(int M, int K) {
     if (M <= 0 || K <= 0 || K % QK) return -1;

@@ -47,6 +47,26 @@ bool device_ok();            // a gfx950 device was opened
             hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                  \
     } while (0)
 
+// Plan and path switches (SLATE_HIP_* environment variables), read when the
+// library initialises and again whenever an engine is created
+// (reload_knobs), so one process can build engines under different settings.
+// The defaults are the measured fastest at the reference's numerics; every
+// setting gives results within the parity tolerances.
+struct Knobs {
+    int attn_wave = 1;     // SLATE_HIP_ATTN_WAVE=0: phased decode attention for every shape
+    int attn_rope = 1;     // SLATE_HIP_ATTN_ROPE: 0 RoPE/append in their own kernel, 2 fused into the phased kernel
+    int q4k_w = 8;         // SLATE_HIP_Q4K_W: waves per decode workgroup (4 or 8)
+    int q4k_r = 0;         // SLATE_HIP_Q4K_R: weight tiles per wave (1, 2, 4; 0 = plan)
+    int q4k_s = 0;         // SLATE_HIP_Q4K_S: decode split count (0 = plan)
+    int q4k_wgs = 448;     // SLATE_HIP_Q4K_WGS: decode workgroup target of the plan
+    int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
+    int q8_r = 0;          // SLATE_HIP_Q8_R, _S, _WGS: the same for the Q8_0 matmul
+    int q8_s = 0;
+    int q8_wgs = 448;
+};
+const Knobs& knobs();
+void reload_knobs();
+
 // Scratch owned by the backend: grown on demand, reused across calls.  Every
 // use happens on the single backend stream, so reuse is ordered.
 void* scratch(int slot, size_t bytes);
@@ -103,6 +123,13 @@ struct Q4kTargets {                 // kernel-argument form
 int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo,
                int64_t split_stride, int max_splits, int* S_out, hipStream_t s,
                hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+// Small-batch Q4_K GEMV (k_q4k_gemv.hip): 1..GEMV_MAX_ROWS activation rows
+// X [B, K] f32 (16-byte aligned rows, ldx floats apart) against up to three
+// tensors (ROW or TILED layout); writes final rows Y[b * ldy + col + m] in
+// one kernel (no operand conversion, no split-K partials).
+constexpr int GEMV_MAX_ROWS = 4;
+int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64_t ldx, int B, int K, float* Y,
+                    int64_t ldy, hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 // TILED weight layout (16-row tiles, see k_q4k.hip).
 size_t q4k_tiled_bytes(int M, int K);
 int launch_q4k_tile(void* dst, const void* src, int M, int K, hipStream_t s);

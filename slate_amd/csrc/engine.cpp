@@ -588,7 +588,10 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             const GroupIn gi = group_in(g, 2);
             Act16 a = act_for(m, T, D);
             rn = RowNorm{nullptr, 0, D, c.rms_eps};
-            if (defer_norm(m, gi, D)) {   // all-Q4_K group: norm factor applied by silu_act
+            // all-Q4_K group: the norm factor is applied by silu_act, which
+            // exists only for widths H % 256 == 0 (the f32 silu_mul
+            // fallback takes no row factor, so other widths normalise here)
+            if (defer_norm(m, gi, D) && H % QK == 0) {
                 rn.ssq = m->ssq;
                 rn.nblk = D / QK;
                 rc = launch_residual_act(m->x, m->part, S, (int64_t)tpad * D, Ld.ffn_norm, T, D, a, m->ssq, s);
@@ -607,7 +610,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             if (H % QK == 0)
                 rc = launch_silu_act(gi.rows() ? m->h : nullptr, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H,
                                      2 * H, gi.q4 ? &a : nullptr, rn, s);
-            else   // no Q4_K operand exists for this width (and no deferred norm: gate/up are not Q4_K)
+            else   // no Q4_K operand exists for this width (and no deferred norm, above)
                 rc = launch_silu_mul(m->h, m->part, m->part + H, T, H, S, (int64_t)tpad * 2 * H, 2 * H, 2 * H, s);
             if (rc) return rc;
             if ((rc = mm_group(m, &a, m->h, T, H, g, col, 1, D, &S, s))) return rc;
@@ -678,6 +681,7 @@ int new_common(slate_hip_llama* m, const slate_hip_llama_config_t* cfg, int max_
     m->cfg = *cfg;
     m->max_slots = max_slots;
     m->max_tokens = max_tokens;
+    reload_knobs();   // the plan switches in force for this engine's steps
     return alloc_runtime(m);
 }
 

@@ -820,10 +820,7 @@ size_t attention_partial_floats(int T, int Hq, int HD, int max_pos) {
 }
 
 // SLATE_HIP_ATTN_WAVE=0 selects the workgroup-phased decode kernel for every shape.
-static bool wave_kernel() {
-    static const bool on = getenv("SLATE_HIP_ATTN_WAVE") == nullptr || atoi(getenv("SLATE_HIP_ATTN_WAVE")) != 0;
-    return on;
-}
+static bool wave_kernel() { return knobs().attn_wave != 0; }
 
 // The wave kernel where its query slices and accumulators fit the registers
 // and the launch is a decode batch (a few query tokens, K/V streamed from
@@ -939,10 +936,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
 // shape (G * HD <= 512, <= 64 tokens) and into the phased kernel elsewhere;
 // 2 always into the phased kernel.  The two fused kernels measured equal
 // on the 8B bench (3781 tok/s each).
-static int rope_fused() {
-    static const int k = getenv("SLATE_HIP_ATTN_ROPE") ? atoi(getenv("SLATE_HIP_ATTN_ROPE")) : 1;
-    return k == 0 || k == 2 ? k : 1;
-}
+static int rope_fused() { return knobs().attn_rope; }
 
 template <int HD, int G, typename KVT>
 static void launch_rope_t(bool wave, dim3 grid, hipStream_t s, hipEvent_t ev0, const void* Kp, const void* Vp,

@@ -12,43 +12,9 @@
 #include "launch.h"
 #include "act16.h"
 #include "mfma.h"
+#include "q4k.h"
 
 namespace slate_hip {
-
-// IEEE half -> float by integer arithmetic (precision.c:10-29 semantics,
-// exact for every input incl. subnormals, independent of FP mode bits).
-__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-    uint32_t sign = (h & 0x8000u) << 16;
-    uint32_t e = (h >> 10) & 0x1fu;
-    uint32_t m = h & 0x3ffu;
-    uint32_t bits;
-    if (e == 0) {
-        if (m == 0) {
-            bits = sign;
-        } else {
-            int sh = __builtin_clz(m) - 21;          // shifts to expose bit 10
-            m = (m << sh) & 0x3ffu;
-            bits = sign | ((uint32_t)(113 - sh) << 23) | (m << 13);
-        }
-    } else if (e == 31) {
-        bits = sign | 0x7f800000u | (m << 13);
-    } else {
-        bits = sign | ((e + 112u) << 23) | (m << 13);
-    }
-    return __uint_as_float(bits);
-}
-
-// Packed 6-bit codes of one block as four bytes per dword (quant.c:157-166):
-// sc_lo holds sub-blocks 0..3, sc_hi 4..7; likewise for mins.
-struct ScaleBytes { uint32_t sc_lo, sc_hi, mn_lo, mn_hi; };
-__device__ __forceinline__ ScaleBytes unpack_scales(uint32_t s0, uint32_t s1, uint32_t s2) {
-    ScaleBytes r;
-    r.sc_lo = s0 & 0x3f3f3f3fu;
-    r.mn_lo = s1 & 0x3f3f3f3fu;
-    r.sc_hi = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
-    r.mn_hi = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
-    return r;
-}
 
 // ---------------------------------------------------------------------------
 // Bit-exact dequant: one thread produces 8 outputs.  Two roundings exactly as
@@ -527,11 +493,6 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     }
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
-
 // Decode plan: the largest R in {4, 2, 1}, then the fewest splits, that give
 // at least `target` workgroups (about two per CU).  Splits keep >= 2 blocks
 // each: a one-block split never overlaps its weight prefetch with compute.
@@ -539,14 +500,13 @@ static int env_int(const char* name, int dflt) {
 // step than 4, since each staged activation block feeds twice the weight
 // tiles, and 16 was 8 % slower); SLATE_HIP_Q4K_W=4 selects four.
 static int dec_waves() {
-    static const int w = env_int("SLATE_HIP_Q4K_W", 8) == 4 ? 4 : 8;
-    return w;
+    return knobs().q4k_w;
 }
 
 static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, int* S_out) {
-    static const int R_env = env_int("SLATE_HIP_Q4K_R", 0);
-    static const int S_env = env_int("SLATE_HIP_Q4K_S", 0);
-    static const int waves_target = env_int("SLATE_HIP_Q4K_WGS", 448) * 4;   // 1792 waves
+    const int R_env = knobs().q4k_r;
+    const int S_env = knobs().q4k_s;
+    const int waves_target = knobs().q4k_wgs * 4;   // 1792 waves by default
     if (s_max > nblk / 2) s_max = nblk / 2;
     if (s_max < 1) s_max = 1;
     int R_out_v = (R_env == 1 || R_env == 2 || R_env == 4) ? R_env : 1, S_out_v = s_max;
@@ -652,7 +612,7 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
             const double cost = (double)rounds * ((double)(nblk + c - 1) / c + 4.0);
             if (cost <= best + 1e-9) { best = cost; S = c; }   // ties: more splits (measured faster)
         }
-        static const int S_env = env_int("SLATE_HIP_Q4K_PF_S", 0);
+        const int S_env = knobs().q4k_pf_s;
         if (S_env > 0) S = std::min(S_env, std::max(1, std::min(max_splits, nblk)));
         const int bps = (nblk + S - 1) / S;
         S = (nblk + bps - 1) / bps;

@@ -360,11 +360,6 @@ __global__ __launch_bounds__(64 * WAVES) void q8_mm_kernel(Q4kTargets tg, const 
     }
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v ? atoi(v) : dflt;
-}
-
 static int cu_count() {
     static int cus = 0;
     if (!cus) {
@@ -414,9 +409,9 @@ int launch_q8(const Q4kTarget* t, int n, const Act8& a, float* out, int64_t ldo,
     if (!a.frag || a.rows_pad < 16 || a.rows_pad % 16) { set_error(-1, "q8_0: bad operand buffer"); return -1; }
     if (max_splits < 1) max_splits = 1;
     const int act_tiles = a.rows_pad / 16;
-    static const int target = env_int("SLATE_HIP_Q8_WGS", 448);
-    static const int R_env = env_int("SLATE_HIP_Q8_R", 0);
-    static const int S_env = env_int("SLATE_HIP_Q8_S", 0);
+    const int target = knobs().q8_wgs;
+    const int R_env = knobs().q8_r;
+    const int S_env = knobs().q8_s;
     int s_cap = std::min(max_splits, std::max(1, ngrp / 2));
     int R = 2, S = 1;
     if (act_tiles == 1) {

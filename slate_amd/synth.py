@@ -191,3 +191,26 @@ def write_llama_gguf(path, shape: LlamaShape, tensors: dict):
     for name, (arr, dt, shp) in tensors.items():
         g.add_tensor(name, shp, {SLATE_Q4_K: GGML_Q4_K, SLATE_Q8_0: GGML_Q8_0}.get(dt, GGML_F32), arr)
     g.write(path)
+
+
+def engine_tensors(m, shape: LlamaShape) -> dict:
+    """The weights of a device engine (slate_amd.Llama) copied back to the
+    host in make_llama's form {name: (array, slate dtype, (out, in) shape)},
+    Q4_K and Q8_0 in slate's row layout, ready for write_llama_gguf or the
+    oracle."""
+    t = {}
+
+    def get(name, key, shp):
+        raw, dt = m.get_tensor(name)
+        t[key] = (raw.view(np.float32) if dt == SLATE_F32 else raw, dt, shp)
+
+    D = shape.d_model
+    get("token_embd", "token_embd.weight", (shape.vocab, D))
+    get("output_norm", "output_norm.weight", (D,))
+    get("output", "output.weight", (shape.vocab, D))
+    for i in range(shape.n_layers):
+        for n in ("attn_norm", "ffn_norm"):
+            get(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", (D,))
+        for n in LINEARS:
+            get(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", linear_shape(shape, n))
+    return t

@@ -11,7 +11,7 @@ import pytest
 
 import slate_amd
 from oracle.pyoracle import OracleModel
-from slate_amd.synth import LlamaShape, make_llama
+from slate_amd.synth import LlamaShape, engine_tensors, make_llama
 from tests.helpers import (N_GEN, Q4, Q4_PROMPT, Q4_SEED, TINY, TINY_SEED, relerr, tensors_digest,
                            tiny_prompts)
 
@@ -522,26 +522,70 @@ def test_mixed_dtype_groups_match_oracle(orc):
     replay_against_oracle(orc, MIXQ, t, m, prompts, 4)
 
 
-def device_model_tensors(m, shape):
-    """Host copy of a device-built model in the make_llama layout (for the oracle)."""
-    t = {}
-
-    def get(name, key, shp):
-        raw, dt = m.get_tensor(name)
-        t[key] = (raw.view(np.float32) if dt == 0 else raw, dt, shp)
-
-    D, kvd, H = shape.d_model, shape.kv_dim, shape.ffn
-    get("token_embd", "token_embd.weight", (shape.vocab, D))
-    get("output_norm", "output_norm.weight", (D,))
-    get("output", "output.weight", (shape.vocab, D))
-    dims = {"attn_q": (D, D), "attn_k": (kvd, D), "attn_v": (kvd, D), "attn_output": (D, D),
-            "ffn_gate": (H, D), "ffn_up": (H, D), "ffn_down": (D, H)}
-    for i in range(shape.n_layers):
-        for n in ("attn_norm", "ffn_norm"):
-            get(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", (D,))
-        for n, shp in dims.items():
-            get(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", shp)
+def requantise(t, kinds, output_kind=None):
+    """Convert the f32 linears of a make_llama model per tensor kind
+    ("q4k" / "q8_0"; others stay f32)."""
+    from slate_amd.synth import quantize_q4k, quantize_q8_0
+    for name in list(t):
+        base = name.rsplit(".", 1)[0].split(".")[-1]
+        kind = output_kind if name == "output.weight" else kinds.get(base)
+        a, _, shp = t[name]
+        if kind == "q4k":
+            t[name] = (np.frombuffer(quantize_q4k(a), np.uint8), 18, shp)
+        elif kind == "q8_0":
+            t[name] = (np.frombuffer(quantize_q8_0(a), np.uint8), 16, shp)
     return t
+
+
+UNALIGNED_FFN = LlamaShape(n_layers=2, d_model=256, n_heads=4, n_kv_heads=2, ffn=352, vocab=300, max_seq=64)
+
+
+def test_q4k_gate_up_with_unaligned_ffn_width(orc):
+    """Q4_K gate/up (K = d_model = 256) with an FFN width that is not a
+    multiple of 256 (352, so down is Q8_0): the SwiGLU falls back to the
+    f32 kernel, which takes no deferred RMSNorm factor, so the FFN norm must
+    be applied before the gate/up matmul; prompt and decode steps against
+    the oracle."""
+    t = make_llama(UNALIGNED_FFN, 55, quant="f32", output_quant="f32")
+    requantise(t, {"attn_q": "q4k", "attn_k": "q4k", "attn_v": "q4k", "attn_output": "q4k",
+                   "ffn_gate": "q4k", "ffn_up": "q4k", "ffn_down": "q8_0"}, "q4k")
+    rng = np.random.default_rng(56)
+    prompts = [rng.integers(0, UNALIGNED_FFN.vocab, n).astype(np.int32) for n in (7, 19, 2)]
+    m = slate_amd.Llama.from_tensors(UNALIGNED_FFN, t, max_slots=3, max_tokens=32)
+    replay_against_oracle(orc, UNALIGNED_FFN, t, m, prompts, 4)
+
+
+# Every non-default setting of the engine's plan and path switches (the
+# f16 K/V cache has its own tolerance study above).  Six sequences, so that
+# decode steps run the 16-row MFMA decode kernels the Q4_K / Q8_0 plan
+# switches steer; a 68-token prompt step for the prompt kernels.
+SWITCHES = [("SLATE_HIP_FUSED_NORM", "0", "q4k"), ("SLATE_HIP_ATTN_TOKENWISE", "0", "q4k"),
+            ("SLATE_HIP_ATTN_WAVE", "0", "q4k"), ("SLATE_HIP_ATTN_ROPE", "0", "q4k"),
+            ("SLATE_HIP_ATTN_ROPE", "2", "q4k"), ("SLATE_HIP_GRAPHS", "1", "q4k"),
+            ("SLATE_HIP_Q4K_R", "1", "q4k"), ("SLATE_HIP_Q4K_R", "4", "q4k"), ("SLATE_HIP_Q4K_W", "4", "q4k"),
+            ("SLATE_HIP_Q4K_S", "1", "q4k"), ("SLATE_HIP_Q4K_S", "3", "q4k"), ("SLATE_HIP_Q4K_WGS", "64", "q4k"),
+            ("SLATE_HIP_Q4K_PF_S", "3", "q4k"), ("SLATE_HIP_Q8_R", "1", "q8_0"), ("SLATE_HIP_Q8_R", "4", "q8_0"),
+            ("SLATE_HIP_Q8_S", "2", "q8_0"), ("SLATE_HIP_Q8_WGS", "64", "q8_0")]
+
+
+@pytest.fixture
+def switch_env(monkeypatch):
+    yield monkeypatch
+    monkeypatch.undo()
+    # the switches are read at engine creation: restore the defaults for
+    # the tests that follow (including those that only call the C ABI)
+    slate_amd.Llama.synthetic(LlamaShape(1, 256, 2, 2, 256, 16, 16), seed=1, quant=0, max_slots=1,
+                              max_tokens=1).free()
+
+
+@pytest.mark.parametrize("name,value,quant", SWITCHES)
+def test_engine_switch_matches_oracle(orc, switch_env, name, value, quant):
+    switch_env.setenv(name, value)
+    t = make_llama(FUSE, 4321, quant=quant, output_quant=quant)
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, FUSE.vocab, n).astype(np.int32) for n in (40, 9, 3, 1, 12, 3)]
+    m = slate_amd.Llama.from_tensors(FUSE, t, max_slots=6, max_tokens=96)
+    replay_against_oracle(orc, FUSE, t, m, prompts, 4)
 
 
 def test_70b_layer_shapes_match_oracle(orc):
@@ -563,7 +607,7 @@ def test_70b_layer_shapes_match_oracle(orc):
         assert rc == 0
         steps.append(lg)
         toks = np.asarray(nxt, np.int32)
-    om = OracleModel(orc, shape, device_model_tensors(m, shape))
+    om = OracleModel(orc, shape, engine_tensors(m, shape))
     for i, p in enumerate(prompts):
         o = om.session()
         rc, want = o.prefill(p)

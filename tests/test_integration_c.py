@@ -1,0 +1,87 @@
+"""The boundary as a C compiler sees it (CPU only, needs slate's include/):
+
+* include/slate_hip.h and slate's include/slate/backend.h in either order,
+  in C11 and C++, with slate's factories (backend.h:104-110) and the HIP
+  one both declared;
+* the loader binding slate_amd/bind/slate_llama_to_hip.c, whose text is the
+  block INTEGRATION.md shows, compiles against slate's llama.h with its
+  struct-layout asserts, and the built binding library exports it.
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+from tests.conftest import ROOT
+
+REF_INCLUDE = "/root/reference/include"
+BIND = os.path.join(ROOT, "slate_amd", "bind", "slate_llama_to_hip.c")
+
+pytestmark = pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="slate's headers are not mounted here")
+
+
+def compile_c(tmp_path, src, lang="c"):
+    f = tmp_path / ("t.c" if lang == "c" else "t.cpp")
+    f.write_text(src)
+    cc = ["gcc", "-std=c11"] if lang == "c" else ["g++", "-std=c++17"]
+    r = subprocess.run(cc + ["-Wall", "-Werror", "-c", "-I", REF_INCLUDE, "-I", os.path.join(ROOT, "include"),
+                             str(f), "-o", str(tmp_path / "t.o")], capture_output=True, text=True)
+    return r.returncode, r.stderr
+
+
+USE_BOTH = """
+const slate_backend_t* pick(void) {
+    const slate_backend_t* b = slate_backend_hip();
+    return b ? b : slate_backend_cpu();
+}
+"""
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+@pytest.mark.parametrize("first", ["slate_hip.h", "slate/backend.h"])
+def test_headers_in_either_order(tmp_path, lang, first):
+    second = "slate/backend.h" if first == "slate_hip.h" else "slate_hip.h"
+    rc, err = compile_c(tmp_path, f'#include "{first}"\n#include "{second}"\n' + USE_BOTH, lang)
+    assert rc == 0, err
+
+
+def test_header_alone_declares_the_vtable(tmp_path):
+    """Without slate's include/ on the path the header declares the struct
+    itself (and never slate's include guard)."""
+    f = tmp_path / "u.c"
+    f.write_text('#include "slate_hip.h"\nconst slate_backend_t* p(void) { return slate_backend_hip(); }\n'
+                 "#ifdef SLATE_BACKEND_H\n#error the slate include guard must stay undefined\n#endif\n")
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-c", "-I", os.path.join(ROOT, "include"), str(f),
+                        "-o", str(tmp_path / "u.o")], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_integration_binding_is_the_shipped_file_and_compiles(tmp_path):
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    sec = doc[doc.index("## 2. The LLaMA path"):doc.index("## 3.")]
+    blocks = re.findall(r"```c\n(.*?)```", sec, flags=re.S)
+    assert blocks and blocks[0] == open(BIND).read()
+    rc, err = compile_c(tmp_path, blocks[0])
+    assert rc == 0, err
+    # two same-typed config fields swapped in a copy of the header (a memcpy
+    # would silently exchange the RoPE base and the RMSNorm epsilon): the
+    # binding's layout asserts reject it
+    hdr = open(os.path.join(ROOT, "include", "slate_hip.h")).read()
+    assert "float theta_base, rms_eps;" in hdr
+    inc = tmp_path / "swapped"
+    inc.mkdir()
+    (inc / "slate_hip.h").write_text(hdr.replace("float theta_base, rms_eps;", "float rms_eps, theta_base;"))
+    f = tmp_path / "b.c"
+    f.write_text(blocks[0])
+    r = subprocess.run(["gcc", "-std=c11", "-c", "-I", REF_INCLUDE, "-I", str(inc), str(f), "-o",
+                        str(tmp_path / "b.o")], capture_output=True, text=True)
+    assert r.returncode != 0 and "theta_base" in r.stderr
+
+
+def test_binding_library_exports_the_binding():
+    so = os.path.join(ROOT, "oracle", "_ref", "libslate_bind.so")
+    if not os.path.exists(so):
+        pytest.skip("oracle/_ref not built")
+    out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True, check=True).stdout
+    assert re.search(r" T slate_llama_to_hip$", out, flags=re.M)

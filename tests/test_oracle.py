@@ -8,6 +8,8 @@ Pins, per oracle function:
                        quantise/dequantise round trip, rotation invariants,
                        tie rules, brute-force packing.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -418,3 +420,64 @@ def test_oracle_bitexact_with_live_reference(orc, ref):
     h = np.arange(0, 31744, 7, dtype=np.uint16)      # finite positive halves
     assert all(np.float32(orc.lib.orc_f16_to_f32(int(v))).view(np.uint32) ==
                np.float32(ref.lib.slate_f16_to_f32(int(v))).view(np.uint32) for v in h)
+
+
+def test_oracle_set_state_continues_a_session(orc):
+    """orc_session_set_state: a fresh session loaded with another session's
+    K/V and position decodes the following tokens bit for bit as that
+    session does (the state is the whole of a session's context); a
+    planted mistake (the position one short) changes the logits."""
+    t = make_llama(Q4, Q4_SEED, quant="q4k", output_quant="f32")
+    m = OracleModel(orc, Q4, t)
+    a = m.session()
+    rc, _ = a.prefill(Q4_PROMPT)
+    assert rc == 0
+    K, V = a.kv()
+    b, c = m.session(), m.session()
+    assert b.set_state(K, V, a.position) == 0 and b.position == a.position
+    assert c.set_state(K, V, a.position - 1) == 0
+    for tok in (3, 41, 9):
+        _, la = a.decode(tok)
+        _, lb = b.decode(tok)
+        assert np.array_equal(bits(la), bits(lb))
+    _, lc = c.decode(3)
+    assert not np.array_equal(bits(lc), bits(m.session().prefill(np.append(Q4_PROMPT, 3))[1]))
+    assert b.set_state(K, V, Q4.max_seq + 1) == -1
+
+
+def test_reference_parallel_decode_equals_sequential(orc, ref, tmp_path):
+    """ref_decode_sessions_parallel (sessions spread over slate's threadpool)
+    gives each session the bits of its own slate_llama_decode_step, and the
+    oracle started from the same K/V states gives them too."""
+    from oracle.pyoracle import RefLlama
+    from slate_amd.synth import write_llama_gguf
+    t = make_llama(Q4, Q4_SEED, quant="q4k", output_quant="f32")
+    path = str(tmp_path / "q4.gguf")
+    write_llama_gguf(path, Q4, t)
+    rm = RefLlama(ref, path)
+    om = OracleModel(orc, Q4, t)
+    try:
+        rng = np.random.default_rng(5)
+        prompts = [rng.integers(0, Q4.vocab, n).astype(np.int32) for n in (3, 9, 1, 5, 12)]
+        par, seq, orcs = [rm.session() for _ in prompts], [rm.session() for _ in prompts], []
+        for p, s1, s2 in zip(prompts, par, seq):
+            assert s1.prefill(p)[0] == 0 and s2.prefill(p)[0] == 0
+            o = om.session()
+            assert o.prefill(p)[0] == 0
+            orcs.append(o)
+        toks = np.array([5, 1, 60, 7, 33], np.int32)
+        n = len(prompts)
+        out = np.empty((n, Q4.vocab), np.float32)
+        rc = np.zeros(n, np.int32)
+        arr = (C.c_void_p * n)(*[s.h for s in par])
+        ref.lib.ref_decode_sessions_parallel(arr, toks.ctypes.data_as(C.POINTER(C.c_int32)), n, fp(out),
+                                             rc.ctypes.data_as(C.POINTER(C.c_int32)))
+        assert not rc.any() and ref.lib.ref_pool_threads() >= 1
+        for i in range(n):
+            want = seq[i].decode(int(toks[i]))[1]
+            assert np.array_equal(bits(out[i]), bits(want))
+            assert np.array_equal(bits(orcs[i].decode(int(toks[i]))[1]), bits(want))
+        for s in par + seq:
+            s.free()
+    finally:
+        rm.close()
