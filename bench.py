@@ -4,34 +4,50 @@
 Workload (one MI355X): 32 layers, d_model 4096, 32 Q / 8 KV heads, head_dim
 128, SwiGLU 14336, vocab 128256; every linear weight Q4_K drawn N(0, 0.02)
 on the device from a fixed seed, embeddings f32, norms 1.  B = 16 sequences;
-contexts prefilled to U[128, 2048] tokens (untimed); each sequence stops after
-U[32, 256] generated tokens and its slot is taken by a new arrival whose
-U[64, 512]-token prompt is prefilled inside the next ragged step (timed, mixed
-prefill + decode).  A step = one pass of the engine over the packed batch;
-each step produces one token per sequence.
+contexts prefilled to U[128, 2048] tokens (untimed); each sequence stops
+after U[32, 256] generated tokens and its slot is taken by a new arrival
+whose U[64, 512]-token prompt is prefilled inside the next ragged step
+(mixed prefill + decode).  The workload starts in steady state: after the
+context prefill each sequence's generated count is drawn uniformly from
+[0, stop), so sequences finish and arrivals come at the steady rate from
+the first timed step on.  A step = one pass of the engine over the packed
+batch; each step produces one token per sequence.
 
-Printed: one JSON line.  value = generated tokens / wall time over K timed
-steps (weights and KV resident in HBM).  roofline = the dominant kernel class
-of the decode steps by device time (decode-shaped Q4_K matmuls or decode
-attention), from HIP events that the kernel dispatches record themselves, in
-every 8th timed step: achieved = algorithmic bytes / device time; traffic =
-HBM bytes per launch from the committed rocprofv3 PMC summary.  cpu_baseline =
-slate's own C decode step (slate_llama_decode_step, single thread as wired)
-on the same weights and KV state, for one step of all 16 sequences.
+Printed: one JSON line.  value = generated tokens / wall time over the K
+timed steps (weights and KV resident in HBM; each step's descriptor upload
+and next-token download are inside).  decode_only_tok_s is the same over
+the steps without prompt chunks.  roofline.step_frac = the timed steps'
+algorithmic bytes (every weight byte once per step, K/V rows read once per
+sequence per step and the new rows written, embedding rows in, logits out)
+/ wall time / 8 TB/s; decode_step_frac the same over decode-only steps.
+roofline.achieved / frac: the dominant kernel class of the decode steps by
+device time (decode-shaped Q4_K matmuls or decode attention), from HIP
+events that the kernel dispatches record themselves, measured in a separate
+window of steps after the timed one (so event recording never slows the
+headline); traffic = HBM bytes per launch from the committed rocprofv3 PMC
+summary.  cpu_baseline = slate's own C decode step (slate_llama_decode_step)
+on the same weights and KV state, one step of the sequences, single thread
+as wired, plus a harness-level variant over slate's threadpool.
 kernels.hbm_copy_GBs = a measured 1 GiB device copy (read + write bytes /
 time) beside the nominal 8 TB/s.
 
+--shape 70b runs the 70B configuration's own workload instead: LLaMA-3-70B
+shapes (80 layers, d_model 8192, 64 Q / 8 KV heads, SwiGLU 28672, vocab
+128256, Q4_K), requests arriving as a Poisson process at 4 per second of
+wall time, prompts U[256, 4096], outputs U[64, 512], greedy, at most 32 in
+flight; prompts are prefilled in chunks inside the ragged steps next to the
+decode rows.  value = generated tokens / wall time over --duration seconds
+after --warmup-s seconds.
+
 --ops instead prints the op-level figures (one JSON object): the Q4_K and
 Q8_0 matmuls through the C ABI (pre-tiled weights) at (M, K) in {(4096, 4096), (14336, 4096), (4096, 14336)}
-and B in {1, 4, 16, 64}, rotating over enough weight copies (> 300 MB) that
-the 256 MB Infinity Cache cannot hold them; and ragged GQA attention with
-B = 64 sequences, 32 q / 8 kv heads, head_dim 128, lengths
+and B in {1, 4, 16, 32, 64}, rotating over enough weight copies (> 300 MB)
+that the 256 MB Infinity Cache cannot hold them; and ragged GQA attention
+with B = 64 sequences, 32 q / 8 kv heads, head_dim 128, lengths
 clip(round(exp(N(ln 1024, 1))), 16, 16384).  Each figure is the device time
 of a captured graph of many calls (no host launch gaps) divided by the calls.
 --copy-calibration instead runs a plain device copy of known size (for
-scaling the PMC byte counters).  --shape 70b runs the same workload with the
-70B layer shapes (80 layers, d_model 8192, 64 Q / 8 KV heads, SwiGLU 28672;
-no CPU baseline, no traffic figure: the PMC summary is of the 8B shape).
+scaling the PMC byte counters).
 """
 import argparse
 import json
@@ -46,15 +62,34 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s at B=16 ragged, 8B-shape Q4_K; Q4_K matmul HBM GB/s"
 HBM_PEAK_GBS = 8000.0
-PROFILE_EVERY = 8
+HOST_THREADS = 16            # the host cores one GPU's share of the box offers
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def weight_bytes(shape):
+    """Algorithmic weight bytes per step: every Q4_K linear and the Q4_K LM
+    head once (slate's 144-byte blocks), the f32 norm vectors once."""
+    D, H, kv = shape.d_model, shape.ffn, shape.kv_dim
+    q4 = lambda M, K: M * (K // 256) * 144
+    per_layer = q4(D, D) * 2 + q4(kv, D) * 2 + q4(H, D) * 2 + q4(D, H) + 2 * D * 4
+    return shape.n_layers * per_layer + q4(shape.vocab, D) + D * 4
+
+
+def step_bytes(shape, pos0, n_new):
+    """Algorithmic HBM bytes of one ragged step: weights once, each sequence's
+    K/V rows 0 .. pos0+n_new-1 read once and its n_new new rows written
+    (2 * layers * kv_dim f32 per row), embedding rows in, logits out."""
+    row = 2 * shape.n_layers * shape.kv_dim * 4
+    T = int(sum(n_new))
+    kv = sum((p + n) * row + n * row for p, n in zip(pos0, n_new))
+    return weight_bytes(shape) + kv + T * shape.d_model * 4 + len(n_new) * shape.vocab * 4
+
+
 class Workload:
-    """Continuous-batching driver over the engine's ragged step."""
+    """Continuous-batching driver over the engine's ragged step (B fixed)."""
 
     def __init__(self, m, shape, B, seed, max_tokens):
         self.m, self.shape, self.B = m, shape, B
@@ -80,9 +115,15 @@ class Workload:
         self.stop[i] = int(self.rng.integers(32, 257))
 
     def prefill_all(self):
-        """Untimed: initial contexts U[128, 2048], packed several per step."""
+        """Untimed: initial contexts U[128, 2048], packed several per step;
+        then each sequence is placed where the steady state of the
+        stop-and-replace process puts it: a slot is found in a sequence of
+        length L with probability proportional to L (length-biased stop), at
+        a uniform point of its generation (gen ~ U[1, stop))."""
+        lens = np.arange(32, 257)
         for i in range(self.B):
             self.start(i, self.new_prompt(128, 2048))
+            self.stop[i] = int(self.rng.choice(lens, p=lens / lens.sum()))
         todo = list(range(self.B))
         while todo:
             group, T = [], 0
@@ -97,11 +138,13 @@ class Workload:
             for i, t in zip(group, nxt):
                 self.pending[i] = None
                 self.last[i] = int(t)
-                self.gen[i] = 1
+                self.gen[i] = 1 + int(self.rng.integers(0, self.stop[i] - 1))
 
     def step(self, want_logits=False):
-        n_new, toks = [], []
+        """One ragged step; returns (mixed, logits, pos0, n_new)."""
+        n_new, toks, pos0 = [], [], []
         for i in range(self.B):
+            pos0.append(self.sess[i].position)
             if self.pending[i] is not None:
                 n_new.append(len(self.pending[i]))
                 toks.append(self.pending[i])
@@ -118,7 +161,216 @@ class Workload:
             if self.gen[i] >= self.stop[i]:
                 self.arrivals += 1
                 self.start(i, self.new_prompt(64, 512))
-        return mixed, lg
+        return mixed, lg, pos0, n_new
+
+
+def run_c4(args, shape):
+    import slate_amd
+    max_tokens = 4096
+    t0 = time.perf_counter()
+    m = slate_amd.Llama.synthetic(shape, seed=args.seed, quant=18, max_slots=args.batch + 1,
+                                  max_tokens=max_tokens)
+    log(f"synthetic 8B-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
+    wl = Workload(m, shape, args.batch, args.seed + 1, max_tokens)
+    t0 = time.perf_counter()
+    wl.prefill_all()
+    ctx0 = [s.position for s in wl.sess]
+    log(f"prefilled {sum(ctx0)} context tokens in {time.perf_counter() - t0:.1f} s")
+    for _ in range(args.warmup):
+        wl.step()
+    lib = slate_amd.load_library()
+    lib.slate_hip_sync()
+    arrivals0 = wl.arrivals
+    step_s, step_mixed, step_by, step_tok = [], [], [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ts = time.perf_counter()
+        mixed, _, pos0, n_new = wl.step()
+        step_s.append(time.perf_counter() - ts)
+        step_mixed.append(mixed)
+        step_by.append(step_bytes(shape, pos0, n_new))
+        step_tok.append(args.batch)
+    lib.slate_hip_sync()
+    dt = time.perf_counter() - t0
+    arrivals = wl.arrivals - arrivals0
+    tokens = int(sum(step_tok))
+    value = tokens / dt
+    dec = [i for i, mx in enumerate(step_mixed) if not mx]
+    dec_s = sum(step_s[i] for i in dec)
+    dec_tok_s = sum(step_tok[i] for i in dec) / dec_s if dec else None
+    step_frac = sum(step_by) / dt / (HBM_PEAK_GBS * 1e9)
+    dec_frac = sum(step_by[i] for i in dec) / dec_s / (HBM_PEAK_GBS * 1e9) if dec else None
+    mix_ms = [round(1e3 * t, 1) for t, mx in zip(step_s, step_mixed) if mx]
+    log(f"{args.steps} steps in {dt:.3f} s, {sum(step_mixed)} mixed ({arrivals} arrivals); decode-only steps "
+        f"{1e3 * np.median([step_s[i] for i in dec]) if dec else 0:.2f} ms median; mixed steps {mix_ms} ms; "
+        f"step_frac {step_frac:.3f}, decode_step_frac {dec_frac if dec_frac is None else round(dec_frac, 3)}")
+    # kernel-class timing in its own window (events recorded by every dispatch)
+    m.profile(True)
+    for _ in range(args.profile_steps):
+        wl.step()
+    m.profile(False)
+    lib.slate_hip_sync()
+    raw = m.profile_read()
+    for k, (ms, by, n) in raw.items():
+        log(f"  {k:13s} {ms:9.2f} ms  {n:6d} launches  {by / max(ms, 1e-9) / 1e6:8.1f} GB/s")
+    dom = max(("q4k_mm", "attention"), key=lambda k: raw[k][0])
+    ms, by, n = raw[dom]
+    achieved = by / (ms * 1e-3) / 1e9
+    kname = "q4k_dec_kernel" if dom == "q4k_mm" else "attn_dec_kernel+attn_merge_kernel"
+    roofline = {"bound": "hbm", "kernel": kname,
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(kname),
+                "launches": n, "avg_launch_us": round(ms * 1e3 / max(n, 1), 2),
+                "algorithmic_bytes_per_launch": round(by / max(n, 1)),
+                "step_frac": round(step_frac, 4),
+                "decode_step_frac": None if dec_frac is None else round(dec_frac, 4),
+                "step_bytes_mean": round(float(np.mean(step_by)))}
+    other = "attention" if dom == "q4k_mm" else "q4k_mm"
+    oms, oby, on = raw[other]
+    step_ms, _, step_n = raw["step"]
+    pf_ms, _, pf_n = raw["q4k_mm_pf"]
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "LLaMA-3-8B-shaped Q4_K decode, ragged continuous batching "
+                               f"B={args.batch} (contexts U[128,2048], stop U[32,256], steady-state "
+                               "arrivals with U[64,512]-token prompts)",
+                   "layers": shape.n_layers, "d_model": shape.d_model,
+                   "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
+                   "weights": "q4_k", "kv_cache": "f16" if lib.slate_hip_llama_kv_f16(m.h) == 1 else "f32",
+                   "batch": args.batch, "mixed_prefill_steps": int(sum(step_mixed)), "arrivals": arrivals,
+                   "mean_context_start": round(float(np.mean(ctx0)), 1)},
+        "decode_only_tok_s": None if dec_tok_s is None else round(dec_tok_s, 1),
+        "roofline": roofline,
+        "kernels": {"profiled_steps": args.profile_steps, "other_decode_class": other,
+                    f"{other}_GBs": round(oby / max(oms, 1e-9) / 1e6, 1), f"{other}_ms": round(oms, 2),
+                    "decode_step_device_ms": round(step_ms / max(step_n, 1), 3),
+                    "decode_step_median_ms": round(1e3 * float(np.median([step_s[i] for i in dec])), 3)
+                    if dec else None,
+                    "mixed_step_ms": mix_ms, "prefill_q4k_ms": round(pf_ms, 2), "prefill_q4k_launches": pf_n},
+    }
+    try:
+        result["kernels"]["hbm_copy_GBs"] = round(copy_bandwidth(), 1)
+    except Exception as e:  # reported beside the nominal peak, never required
+        result["kernels"]["hbm_copy_GBs"] = None
+        log(f"copy bandwidth not measured: {e}")
+    if not args.no_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline_and_parity(m, shape, wl)
+        except Exception as e:  # the baseline is reported, never required
+            result["cpu_baseline"] = {"error": str(e)}
+    return result
+
+
+class PoissonWorkload:
+    """Open-loop serving: requests arrive as a Poisson process in wall time,
+    wait for one of max_batch slots, prefill their prompt in chunks inside
+    the ragged steps (the step's token budget minus its decode rows) and
+    then decode until their output length."""
+
+    def __init__(self, m, shape, max_batch, rate, seed, max_tokens, prompt=(256, 4096), out=(64, 512)):
+        self.m, self.shape, self.max_batch, self.rate = m, shape, max_batch, rate
+        self.rng = np.random.default_rng(seed)
+        self.max_tokens, self.prompt_rng, self.out_rng = max_tokens, prompt, out
+        self.queue, self.active = [], []
+        self.next_arrival = float(self.rng.exponential(1.0 / rate))
+        self.arrived = self.completed = self.generated = 0
+
+    def admit(self, now):
+        while self.next_arrival <= now:
+            n = int(self.rng.integers(self.prompt_rng[0], self.prompt_rng[1] + 1))
+            self.queue.append({"prompt": self.rng.integers(0, self.shape.vocab, n).astype(np.int32),
+                               "out": int(self.rng.integers(self.out_rng[0], self.out_rng[1] + 1)),
+                               "t": self.next_arrival})
+            self.arrived += 1
+            self.next_arrival += float(self.rng.exponential(1.0 / self.rate))
+        while self.queue and len(self.active) < self.max_batch:
+            r = self.queue.pop(0)
+            r.update(sess=self.m.session(), done=0, gen=0, last=0)
+            self.active.append(r)
+
+    def step(self, now):
+        """One ragged step at wall time `now`; returns (tokens generated, step ran)."""
+        self.admit(now)
+        if not self.active:
+            return 0, False
+        budget = self.max_tokens - sum(1 for r in self.active if r["done"] == len(r["prompt"]))
+        rows, n_new, toks = [], [], []
+        for r in self.active:
+            left = len(r["prompt"]) - r["done"]
+            if left == 0:
+                rows.append(r)
+                n_new.append(1)
+                toks.append(np.array([r["last"]], np.int32))
+            elif budget > 0:
+                c = min(left, budget)
+                budget -= c
+                rows.append(r)
+                n_new.append(c)
+                toks.append(r["prompt"][r["done"]:r["done"] + c])
+        rc, _, nxt = self.m.step([r["sess"] for r in rows], n_new, np.concatenate(toks), want_logits=False)
+        assert rc == 0, f"step rc={rc}"
+        gen = 0
+        for r, n, t in zip(rows, n_new, nxt):
+            if r["done"] < len(r["prompt"]):
+                r["done"] += n
+                if r["done"] < len(r["prompt"]):
+                    continue                       # prompt not finished: no token yet
+            r["last"] = int(t)
+            r["gen"] += 1
+            gen += 1
+        for r in [r for r in self.active if r["gen"] >= r["out"]]:
+            r["sess"].free()
+            self.active.remove(r)
+            self.completed += 1
+        self.generated += gen
+        return gen, True
+
+
+def run_c5(args, shape):
+    import slate_amd
+    max_tokens, max_batch, rate = 4096, 32, 4.0
+    t0 = time.perf_counter()
+    m = slate_amd.Llama.synthetic(shape, seed=args.seed, quant=18, max_slots=max_batch, max_tokens=max_tokens)
+    log(f"synthetic 70B-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
+    wl = PoissonWorkload(m, shape, max_batch, rate, args.seed + 1, max_tokens)
+    lib = slate_amd.load_library()
+    start = time.perf_counter()
+    now = 0.0
+    while now < args.warmup_s:                     # fill the system from empty
+        wl.step(now)
+        now = time.perf_counter() - start
+    lib.slate_hip_sync()
+    g0, a0, c0 = wl.generated, wl.arrived, wl.completed
+    steps, batch_sum, t_begin = 0, 0, time.perf_counter()
+    while time.perf_counter() - t_begin < args.duration:
+        now = time.perf_counter() - start
+        ran = wl.step(now)[1]
+        steps += ran
+        batch_sum += len(wl.active)
+        if not ran:
+            time.sleep(0.001)
+    lib.slate_hip_sync()
+    dt = time.perf_counter() - t_begin
+    tokens = wl.generated - g0
+    log(f"{steps} steps in {dt:.1f} s: {tokens} tokens, {wl.arrived - a0} arrivals, "
+        f"{wl.completed - c0} completed, mean batch {batch_sum / max(steps, 1):.1f}, queue {len(wl.queue)}")
+    return {
+        "metric": "generated tok/s, 70B-shape Q4_K, Poisson 4 req/s, B<=32 (mixed prefill + decode)",
+        "value": round(tokens / dt, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup_s": args.warmup_s,
+        "duration_s": round(dt, 2), "ms_per_step": round(dt * 1e3 / max(steps, 1), 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "LLaMA-3-70B-shaped Q4_K serving: Poisson arrivals at 4 req/s, prompts "
+                               "U[256,4096], outputs U[64,512], greedy, at most 32 in flight, prompts "
+                               "chunked into the ragged steps (4096-token budget)",
+                   "layers": shape.n_layers, "d_model": shape.d_model,
+                   "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
+                   "weights": "q4_k", "max_batch": max_batch, "arrivals": wl.arrived - a0,
+                   "completed": wl.completed - c0, "mean_batch": round(batch_sum / max(steps, 1), 2),
+                   "queued_at_end": len(wl.queue)},
+    }
 
 
 def main():
@@ -126,10 +378,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--profile-steps", type=int, default=8, help="event-timed steps after the timed window")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--layers", type=int, default=None, help="layers (default: the shape's own)")
     ap.add_argument("--shape", choices=("8b", "70b"), default="8b",
-                    help="model shape: 8b (the headline line) or 70b (same workload, 70B layer shapes)")
+                    help="8b (the headline line) or 70b (the 70B serving workload)")
+    ap.add_argument("--duration", type=float, default=60.0, help="70b: timed seconds")
+    ap.add_argument("--warmup-s", type=float, default=20.0, help="70b: untimed seconds from an empty system")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -157,112 +412,15 @@ def main():
         import torch  # noqa: F401
     except ImportError:
         pass
-
-    import slate_amd
     from slate_amd.synth import LlamaShape
-    big = args.shape == "70b"
-    if args.layers is None:
-        args.layers = 80 if big else 32
-    if big:
-        shape = LlamaShape(n_layers=args.layers, d_model=8192, n_heads=64, n_kv_heads=8, ffn=28672,
-                           vocab=128256, max_seq=2304)
-        args.no_cpu = True    # the reference's C decode step needs ~13 s per token per core at this shape
+    if args.shape == "70b":
+        shape = LlamaShape(n_layers=args.layers or 80, d_model=8192, n_heads=64, n_kv_heads=8, ffn=28672,
+                           vocab=128256, max_seq=4096 + 512)
+        result = run_c5(args, shape)
     else:
-        shape = LlamaShape(n_layers=args.layers, d_model=4096, n_heads=32, n_kv_heads=8, ffn=14336,
+        shape = LlamaShape(n_layers=args.layers or 32, d_model=4096, n_heads=32, n_kv_heads=8, ffn=14336,
                            vocab=128256, max_seq=2304)
-    max_tokens = 4096
-    t0 = time.perf_counter()
-    m = slate_amd.Llama.synthetic(shape, seed=args.seed, quant=18, max_slots=args.batch + 1,
-                                  max_tokens=max_tokens)
-    log(f"synthetic {args.shape.upper()}-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
-    wl = Workload(m, shape, args.batch, args.seed + 1, max_tokens)
-    t0 = time.perf_counter()
-    wl.prefill_all()
-    ctx0 = [s.position for s in wl.sess]
-    log(f"prefilled {sum(ctx0)} context tokens in {time.perf_counter() - t0:.1f} s")
-    for _ in range(args.warmup):
-        wl.step()
-    lib = slate_amd.load_library()
-    m.profile(True)
-    m.profile(False)
-    lib.slate_hip_sync()
-    arrivals0 = wl.arrivals
-    mixed_steps = 0
-    step_s, step_mixed, step_prof = [], [], []
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        # one step in PROFILE_EVERY is launched kernel by kernel with
-        # dispatch-recorded events (the roofline); the others replay graphs
-        prof = i % PROFILE_EVERY == 0
-        if prof:
-            m.profile(True, reset=False)
-        ts = time.perf_counter()
-        mixed = wl.step()[0]
-        step_s.append(time.perf_counter() - ts)
-        if prof:
-            m.profile(False)
-        step_mixed.append(mixed)
-        step_prof.append(prof)
-        mixed_steps += mixed
-    lib.slate_hip_sync()
-    dt = time.perf_counter() - t0
-    raw = m.profile_read()
-    tokens = args.batch * args.steps
-    value = tokens / dt
-    dec_s = [t for t, mx, p in zip(step_s, step_mixed, step_prof) if not mx and not p]
-    mix_s = [t for t, mx in zip(step_s, step_mixed) if mx]
-    log(f"{args.steps} steps in {dt:.3f} s, {mixed_steps} with arrivals ({wl.arrivals - arrivals0} arrivals); "
-        f"decode-only step median {1e3 * np.median(dec_s) if dec_s else 0:.2f} ms, "
-        f"mixed steps {[round(1e3 * t, 1) for t in mix_s]} ms")
-    for k, (ms, by, n) in raw.items():
-        log(f"  {k:13s} {ms:9.2f} ms  {n:6d} launches  {by / max(ms, 1e-9) / 1e6:8.1f} GB/s")
-    # roofline: the dominant kernel class of the decode steps by device time
-    # (decode-shaped Q4_K matmuls vs decode attention)
-    dom = max(("q4k_mm", "attention"), key=lambda k: raw[k][0])
-    ms, by, n = raw[dom]
-    achieved = by / (ms * 1e-3) / 1e9
-    kname = "q4k_dec_kernel" if dom == "q4k_mm" else "attn_dec_kernel+attn_merge_kernel"
-    roofline = {"bound": "hbm", "kernel": kname,
-                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": None if big else measured_traffic(kname),   # the PMC summary is of the 8B shape
-                "launches": n, "avg_launch_us": round(ms * 1e3 / max(n, 1), 2),
-                "algorithmic_bytes_per_launch": round(by / max(n, 1))}
-    other = "attention" if dom == "q4k_mm" else "q4k_mm"
-    oms, oby, on = raw[other]
-    step_ms, _, step_n = raw["step"]
-    pf_ms, pf_by, pf_n = raw["q4k_mm_pf"]
-    result = {
-        "metric": METRIC.replace("8B-shape", "70B-shape") if big else METRIC, "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": ("LLaMA-70B-shaped" if big else "LLaMA-3-8B-shaped") +
-                               f" Q4_K decode, ragged continuous batching B={args.batch} "
-                               "(contexts U[128,2048], stop U[32,256], arrivals with U[64,512]-token prompts)",
-                   "layers": args.layers, "d_model": shape.d_model,
-                   "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
-                   "weights": "q4_k", "kv_cache": "f16" if lib.slate_hip_llama_kv_f16(m.h) == 1 else "f32",
-                   "batch": args.batch,
-                   "mixed_prefill_steps": mixed_steps, "arrivals": wl.arrivals - arrivals0,
-                   "mean_context_start": round(float(np.mean(ctx0)), 1)},
-        "roofline": roofline,
-        "kernels": {"other_decode_class": other, f"{other}_GBs": round(oby / max(oms, 1e-9) / 1e6, 1),
-                    f"{other}_ms": round(oms, 2),
-                    "decode_step_device_ms": round(step_ms / max(step_n, 1), 3),
-                    "decode_step_median_ms": round(1e3 * float(np.median(dec_s)), 3) if dec_s else None,
-                    "mixed_step_ms": [round(1e3 * t, 1) for t in mix_s],
-                    "prefill_q4k_ms": round(pf_ms, 2), "prefill_q4k_launches": pf_n},
-    }
-    try:
-        result["kernels"]["hbm_copy_GBs"] = round(copy_bandwidth(), 1)
-    except Exception as e:  # reported beside the nominal peak, never required
-        result["kernels"]["hbm_copy_GBs"] = None
-        log(f"copy bandwidth not measured: {e}")
-    if not args.no_cpu:
-        try:
-            result["cpu_baseline"] = cpu_baseline_and_parity(m, shape, wl)
-        except Exception as e:  # the baseline is reported, never required
-            result["cpu_baseline"] = {"error": str(e)}
+        result = run_c4(args, shape)
     print(json.dumps(result), flush=True)
     return 0
 
@@ -348,7 +506,7 @@ def run_ops(seed):
                 slate_amd.check(tile(copies[c].data_ptr(), raw.data_ptr(), M, K), fmt + " tile")
             lib.slate_hip_sync()
             del raw
-            for B in (1, 4, 16, 64):
+            for B in (1, 4, 16, 32, 64):
                 X = torch.randn(B, K, device="cuda", generator=gen)
                 Y = torch.empty(B, M, device="cuda")
                 torch.cuda.synchronize()
@@ -409,52 +567,34 @@ def measured_traffic(kernel):
 
 
 def cpu_baseline_and_parity(m, shape, wl):
-    """Snapshot KV of every decoding sequence, run the CPU reference step from
-    that state, then the GPU step; compare the two sets of logits."""
-    snap = [(i, wl.sess[i].kv(), wl.sess[i].position, wl.last[i]) for i in range(wl.B)
-            if wl.pending[i] is None]
-    _, lg, _ = wl.m.step([wl.sess[i] for i, *_ in snap], [1] * len(snap),
-                         [t for *_, t in snap], want_logits=True)
-    gpu = {i: lg[k] for k, (i, *_) in enumerate(snap)}
-    return cpu_baseline_from(m, shape, snap, gpu)
+    """Snapshot the KV of every decoding sequence, run slate's C decode step
+    from that state (single thread as wired, then the harness-level
+    threadpool variant), then the GPU step; compare the logits."""
+    snap = [i for i in range(wl.B) if wl.pending[i] is None]
+    kv = {i: (wl.sess[i].kv(), wl.sess[i].position, wl.last[i]) for i in snap}
+    _, lg, _ = wl.m.step([wl.sess[i] for i in snap], [1] * len(snap), [wl.last[i] for i in snap],
+                         want_logits=True)
+    gpu = {i: lg[k] for k, i in enumerate(snap)}
+    return cpu_baseline_from(m, shape, [(i, *kv[i]) for i in snap], gpu)
 
 
-def cpu_baseline_from(m, shape, snap, gpu, budget_s=40.0):
+def cpu_baseline_from(m, shape, snap, gpu, budget_s=30.0):
+    """slate_llama_decode_step (oracle/_ref) on the engine's weights and the
+    given KV states: one session at a time on one thread (as slate wires
+    it), then all of them over slate's own threadpool (harness level)."""
+    host_threads = min(HOST_THREADS, len(os.sched_getaffinity(0)))
+    os.environ.setdefault("SLATE_NUM_THREADS", str(host_threads))
     from oracle.pyoracle import Ref, RefLlama, ref_available
-    from slate_amd.gguf import GGML_F32, GGML_Q4_K, GGUFWriter
+    import slate_amd
+    from slate_amd.synth import engine_tensors, write_llama_gguf
     if not ref_available():
         return {"error": "oracle/_ref not built"}
     ref = Ref()
-    path = "/dev/shm/slate_amd_bench_8b.gguf"
-    g = GGUFWriter()
-    g.add_str("general.architecture", "llama")
-    for k, v in (("block_count", shape.n_layers), ("embedding_length", shape.d_model),
-                 ("feed_forward_length", shape.ffn), ("attention.head_count", shape.n_heads),
-                 ("attention.head_count_kv", shape.n_kv_heads), ("context_length", shape.max_seq),
-                 ("vocab_size", shape.vocab)):
-        g.add_u32("llama." + k, v)
-    g.add_f32("llama.rope.freq_base", shape.theta)
-    g.add_f32("llama.attention.layer_norm_rms_epsilon", shape.eps)
-    D, H, kv = shape.d_model, shape.ffn, shape.kv_dim
-    dims = {"attn_q": (D, D), "attn_k": (kv, D), "attn_v": (kv, D), "attn_output": (D, D),
-            "ffn_gate": (H, D), "ffn_up": (H, D), "ffn_down": (D, H)}
-
-    def add(name, gname, shp):
-        raw, dt = m.get_tensor(name)
-        g.add_tensor(gname, shp, GGML_Q4_K if dt == 18 else GGML_F32, raw)
-
-    add("token_embd", "token_embd.weight", (shape.vocab, D))
-    add("output_norm", "output_norm.weight", (D,))
-    add("output", "output.weight", (shape.vocab, D))
-    for i in range(shape.n_layers):
-        add(f"blk.{i}.attn_norm", f"blk.{i}.attn_norm.weight", (D,))
-        add(f"blk.{i}.ffn_norm", f"blk.{i}.ffn_norm.weight", (D,))
-        for n, shp in dims.items():
-            add(f"blk.{i}.{n}", f"blk.{i}.{n}.weight", shp)
-    g.write(path)
-    del g
+    path = "/dev/shm/slate_amd_bench.gguf"
+    write_llama_gguf(path, shape, engine_tensors(m, shape))
     rm = RefLlama(ref, path)
     t_cpu, n_tok, worst = 0.0, 0, 0.0
+    pool = {}
     try:
         for i, (K, V), pos, tok in snap:
             rs = rm.session()
@@ -468,6 +608,29 @@ def cpu_baseline_from(m, shape, snap, gpu, budget_s=40.0):
             worst = max(worst, float(np.abs(lg - gpu[i]).max() / max(np.abs(lg).max(), 1e-30)))
             if t_cpu > budget_s:
                 break
+        # harness level: every snapshot session decoded at once over the pool
+        rss = []
+        for i, (K, V), pos, tok in snap:
+            rs = rm.session()
+            assert rs.set_state(K, V, pos) == 0
+            rss.append(rs)
+        n = len(rss)
+        toks = np.array([tok for *_, tok in snap], np.int32)
+        out = np.empty((n, shape.vocab), np.float32)
+        rcs = np.zeros(n, np.int32)
+        arr = (slate_amd.vp * n)(*[r.h for r in rss])
+        t0 = time.perf_counter()
+        ref.lib.ref_decode_sessions_parallel(arr, toks.ctypes.data_as(slate_amd.i32p), n,
+                                             out.ctypes.data_as(slate_amd.f32p), rcs.ctypes.data_as(slate_amd.i32p))
+        tp = time.perf_counter() - t0
+        assert not rcs.any()
+        for k, (i, *_rest) in enumerate(snap):
+            worst = max(worst, float(np.abs(out[k] - gpu[i]).max() / max(np.abs(out[k]).max(), 1e-30)))
+        for r in rss:
+            r.free()
+        pool = dict(value=round(n / tp, 4), unit="tok/s", cores=int(ref.lib.ref_pool_threads()),
+                    sample=f"one decode step of {n} sequences, sessions spread over slate_threadpool_parallel_for "
+                           f"(threadpool.c:122-142; harness-level, not wired in slate's LLaMA path), {tp:.1f} s")
     finally:
         rm.close()
         os.unlink(path)
@@ -475,7 +638,8 @@ def cpu_baseline_from(m, shape, snap, gpu, budget_s=40.0):
                 sample=f"slate_llama_decode_step (slate's C, built from its sources, single thread as wired) "
                        f"on the benchmark's weights and KV state: one decode step of {n_tok} sequences, "
                        f"{t_cpu:.1f} s",
-                host_cores_available=os.cpu_count(), host_cpu=cpu_model(), logits_max_rel_vs_gpu=worst)
+                threadpool=pool, host_cores_available=len(os.sched_getaffinity(0)),
+                host_cores_used_max=host_threads, host_cpu=cpu_model(), logits_max_rel_vs_gpu=worst)
 
 
 def cpu_model():

@@ -220,6 +220,8 @@ slate_hip_llama_t* slate_hip_llama_new_synthetic(const slate_hip_llama_config_t*
                                                  uint64_t seed, int quant,
                                                  int max_slots, int max_tokens);
 void  slate_hip_llama_free(slate_hip_llama_t* m);
+/* The model's config (llama.h:98 slate_llama_config); NULL for NULL. */
+const slate_hip_llama_config_t* slate_hip_llama_config(const slate_hip_llama_t* m);
 /* Copy a weight tensor back to host ("token_embd", "output", "output_norm",
  * or "blk.N.<name>"); returns bytes written or a negative code. */
 int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
@@ -231,6 +233,9 @@ int64_t slate_hip_llama_get_tensor(const slate_hip_llama_t* m, const char* name,
 slate_hip_llama_session_t* slate_hip_llama_session_new(slate_hip_llama_t* m);
 void  slate_hip_llama_session_free(slate_hip_llama_session_t* s);
 int   slate_hip_llama_session_position(const slate_hip_llama_session_t* s);
+/* Back to position 0 for a new conversation, keeping the KV slot
+ * (slate_infer_session_reset, infer.h:116, engine.c:429-431). */
+void  slate_hip_llama_session_reset(slate_hip_llama_session_t* s);
 int   slate_hip_llama_prefill(slate_hip_llama_session_t* s, const int32_t* tokens,
                               int n_tokens, float* out_logits);
 int   slate_hip_llama_decode_step(slate_hip_llama_session_t* s, int32_t token,

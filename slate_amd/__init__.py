@@ -104,6 +104,8 @@ SIGNATURES = {
     "slate_hip_llama_session_new": (vp, [vp]),
     "slate_hip_llama_session_free": (None, [vp]),
     "slate_hip_llama_session_position": (C.c_int, [vp]),
+    "slate_hip_llama_session_reset": (None, [vp]),
+    "slate_hip_llama_config": (C.POINTER(LlamaConfig), [vp]),
     "slate_hip_llama_prefill": (C.c_int, [vp, vp, C.c_int, vp]),
     "slate_hip_llama_decode_step": (C.c_int, [vp, C.c_int32, vp]),
     "slate_hip_llama_step": (C.c_int, [vp, vp, C.c_int, vp, vp, vp, vp]),

@@ -107,6 +107,7 @@ void reload_knobs() {
     k.q4k_s = std::max(0, env_int("SLATE_HIP_Q4K_S", 0));
     k.q4k_wgs = std::max(1, env_int("SLATE_HIP_Q4K_WGS", 448));
     k.q4k_pf_s = std::max(0, env_int("SLATE_HIP_Q4K_PF_S", 0));
+    k.q4k_dec32 = env_int("SLATE_HIP_Q4K_DEC32", 1) != 0;
     k.q8_r = env_int("SLATE_HIP_Q8_R", 0);
     if (k.q8_r != 1 && k.q8_r != 2 && k.q8_r != 4) k.q8_r = 0;
     k.q8_s = std::max(0, env_int("SLATE_HIP_Q8_S", 0));
@@ -251,8 +252,8 @@ static int matmul_q4k_common(float* Y, const void* A, const float* X, int B, int
     SH_REQUIRE(K % QK == 0, "matmul_q4k: K=%d is not a multiple of 256", K);
     std::lock_guard<std::mutex> lk(g_enqueue_mu);
     Q4kTarget t{A, M, 0};
-    // a few rows: one GEMV kernel straight into Y (no operand, no partials)
-    if (B <= GEMV_MAX_ROWS && ((uintptr_t)X & 15) == 0)
+    // one row: one GEMV kernel straight into Y (no operand, no partials)
+    if (B <= GEMV_ROUTE_ROWS && ((uintptr_t)X & 15) == 0)
         return launch_q4k_gemv(&t, 1, tiled, X, K, B, K, Y, M, g_stream);
     Act16 a;
     if (make_act16(a, B, K, 0)) return -2;
@@ -274,7 +275,6 @@ int slate_hip_matmul_q4k(float* Y, const void* A, const float* X, int B, int M, 
 int slate_hip_matmul_q4k_tiled(float* Y, const void* A, const float* X, int B, int M, int K) {
     return matmul_q4k_common(Y, A, X, B, M, K, true);
 }
-
 
 int64_t slate_hip_q4k_tiled_bytes(int M, int K) {
     if (M <= 0 || K <= 0 || K % QK) return -1;

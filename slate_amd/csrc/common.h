@@ -60,6 +60,7 @@ struct Knobs {
     int q4k_s = 0;         // SLATE_HIP_Q4K_S: decode split count (0 = plan)
     int q4k_wgs = 448;     // SLATE_HIP_Q4K_WGS: decode workgroup target of the plan
     int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
+    int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one
     int q8_r = 0;          // SLATE_HIP_Q8_R, _S, _WGS: the same for the Q8_0 matmul
     int q8_s = 0;
     int q8_wgs = 448;
@@ -128,6 +129,12 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
 // tensors (ROW or TILED layout); writes final rows Y[b * ldy + col + m] in
 // one kernel (no operand conversion, no split-K partials).
 constexpr int GEMV_MAX_ROWS = 4;
+// The C ABI's Q4_K matmuls take the GEMV for a single activation row: the
+// VALU dot products cost ~2.9 wave-lane operations per weight element
+// (a wave64 f32 operation takes 4 cycles of a SIMD) against ~1 for building
+// the MFMA operand, so from two rows on the one-kernel GEMV no longer beats
+// the three-kernel MFMA path (operand conversion, matmul, split sum).
+constexpr int GEMV_ROUTE_ROWS = 1;
 int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64_t ldx, int B, int K, float* Y,
                     int64_t ldy, hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 // TILED weight layout (16-row tiles, see k_q4k.hip).

@@ -919,6 +919,14 @@ void slate_hip_llama_session_free(slate_hip_llama_session_t* s) {
 
 int slate_hip_llama_session_position(const slate_hip_llama_session_t* s) { return s ? s->pos : -1; }
 
+void slate_hip_llama_session_reset(slate_hip_llama_session_t* s) {
+    if (!s) return;
+    std::lock_guard<std::mutex> lk(s->m->mu);
+    s->pos = 0;   // attention reads positions < pos only: stale K/V rows are never read
+}
+
+const slate_hip_llama_config_t* slate_hip_llama_config(const slate_hip_llama_t* m) { return m ? &m->cfg : nullptr; }
+
 int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessions, int n, const int32_t* n_new,
                          const int32_t* tokens, float* out_logits, int32_t* out_next) {
     if (!m || !sessions || !n_new || !tokens || n < 1 || n > m->max_slots) return -1;

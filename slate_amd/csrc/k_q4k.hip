@@ -190,21 +190,24 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
     return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
-// Decode kernel (one 16-row activation tile).  A workgroup of WAVES waves
-// owns WAVES*R weight tiles (possibly spread over up to three fused tensors) and
-// one split of super-blocks.  The activation units of a block are copied
-// into a double-buffered LDS tile by direct global->LDS loads, one block
-// ahead and issued before the next block's weight loads; each wave holds its
-// R weight tiles in registers, loaded one block ahead; every step ends with
-// one wait for all loads and one barrier.  W and frag are not __restrict__:
-// loads through restrict pointers count as invariant and may be moved across
-// the barriers that order them here.
-template <int R, bool TILED, int WAVES = 4>
+// Decode kernel (NT = 1 or 2 16-row activation tiles: up to 32 rows).  A
+// workgroup of WAVES waves owns WAVES*R weight tiles (possibly spread over
+// up to three fused tensors) and one split of super-blocks.  The NT tiles'
+// activation units of a block are copied into a double-buffered LDS area by
+// direct global->LDS loads, one block ahead and issued before the next
+// block's weight loads; each wave holds its R weight tiles in registers,
+// loaded one block ahead, and builds each tile's B operand once per K step
+// for all NT activation tiles; every step ends with one wait for all loads
+// and one barrier.  W and frag are not __restrict__: loads through restrict
+// pointers count as invariant and may be moved across the barriers that
+// order them here.
+template <int R, bool TILED, int WAVES = 4, int NT = 1>
 __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, const uint4* frag,
                                                              float* __restrict__ out, int64_t ldo,
                                                              int64_t split_stride, int nblk, int bps) {
-    __shared__ uint4 s_act[2 * ACT_FRAG_UNITS];
-    constexpr int CHUNKS = ACT_FRAG_UNITS / 64;       // 1 KiB wave copies per block
+    __shared__ uint4 s_act[2 * NT * ACT_FRAG_UNITS];
+    constexpr int TCH = ACT_FRAG_UNITS / 64;          // 1 KiB wave copies per tile and block
+    constexpr int CHUNKS = NT * TCH;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int j = lane & 15;
@@ -234,20 +237,26 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
         if (TILED) load_wtile_tiled(w, wp[r] + (size_t)kb * (16 * QBLOCK), lane);
         else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
     };
-    // copy block kb's units (kb < nblk: inside the operand buffer) into dst
+    // copy block kb's units of the NT tiles (kb < nblk: inside the operand
+    // buffer, tile n's block at (n * nblk + kb) units) into dst
     const uint32_t o_act = 16 * lane;
     auto stage = [&](uint4* dst, int kb) {
-        const uint4* src = frag + (size_t)kb * ACT_FRAG_UNITS;
 #pragma unroll
         for (int i = 0; i < (CHUNKS + WAVES - 1) / WAVES; ++i) {
             const int c = wv + WAVES * i;
-            if (c < CHUNKS) lds_copy16(src + c * 64, o_act, lds_addr(dst + c * 64));
+            if (c < CHUNKS) {
+                const int n = c / TCH, u = (c - n * TCH) * 64;
+                lds_copy16(frag + ((size_t)n * nblk + kb) * ACT_FRAG_UNITS + u, o_act,
+                           lds_addr(dst + n * ACT_FRAG_UNITS + u));
+            }
         }
     };
     WTile w0[R], w1[R];
-    floatx4 acc[R];
+    floatx4 acc[R][NT];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     stage(s_act, kb0);
     __builtin_amdgcn_sched_barrier(0);
@@ -259,44 +268,56 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
     // block b from wc (landed) while wn receives block b+1; the two register
     // sets swap roles each step (the loop is unrolled by two)
     auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
-        const uint4* cur = s_act + (b & 1) * ACT_FRAG_UNITS;
+        const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
         if (b + 1 < nb) {                               // the last block prefetches nothing
-            stage(s_act + ((b + 1) & 1) * ACT_FRAG_UNITS, kb0 + b + 1);
+            stage(s_act + ((b + 1) & 1) * NT * ACT_FRAG_UNITS, kb0 + b + 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < R; ++r) ldw(wn[r], r, kb0 + b + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
         if (active) {
-            // one K step at a time: the step's activation fragment is read
-            // once and each tile's B operand is built right before its MFMAs
+            // one K step at a time: each tile's B operand is built once and
+            // run against the NT activation fragments of the step
             WScale cs[R];
-            floatx4 am[R];
+            floatx4 am[R][NT];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 cs[r] = q4k_wscale(wc[r], g);
-                am[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int n = 0; n < NT; ++n) am[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const half8_t h = __builtin_bit_cast(half8_t, cur[(2 * t) * 64 + lane]);
-                const half8_t l = __builtin_bit_cast(half8_t, cur[(2 * t + 1) * 64 + lane]);
+                half8_t bop[R];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const half8_t bop = q4k_bop(wc[r], cs[r], t);
-                    am[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bop, am[r], 0, 0, 0);
-                    am[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bop, am[r], 0, 0, 0);
+                for (int r = 0; r < R; ++r) bop[r] = q4k_bop(wc[r], cs[r], t);
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const uint4* sa = cur + n * ACT_FRAG_UNITS;
+                    const half8_t h = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
+                    const half8_t l = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bop[r], am[r][n], 0, 0, 0);
+                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bop[r], am[r][n], 0, 0, 0);
+                    }
                 }
             }
-            const half4_t ys = *(const half4_t*)(cur + 1024 + lane);
-            const float4 rv = __builtin_bit_cast(float4, cur[1088 + g]);
-            const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                floatx4 an = {0.f, 0.f, 0.f, 0.f};
-                an = __builtin_amdgcn_mfma_f32_16x16x16f16(ys, cs[r].bmin, an, 0, 0, 0);
+            for (int n = 0; n < NT; ++n) {
+                const uint4* sa = cur + n * ACT_FRAG_UNITS;
+                const half4_t ys = *(const half4_t*)(sa + 1024 + lane);
+                const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
+                const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[r][i] += (cs[r].d * am[r][i] - cs[r].dmin64 * an[i]) * rs[i];
+                for (int r = 0; r < R; ++r) {
+                    floatx4 an = {0.f, 0.f, 0.f, 0.f};
+                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ys, cs[r].bmin, an, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[r][n][i] += (cs[r].d * am[r][n][i] - cs[r].dmin64 * an[i]) * rs[i];
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -316,7 +337,9 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
         const int row = (tile0 + r) * 16 + j;
         if (tile0 + r < tiles && row < M) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[(int64_t)(4 * g + i) * ldo + row] = acc[r][i];
+            for (int n = 0; n < NT; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[(int64_t)(16 * n + 4 * g + i) * ldo + row] = acc[r][n][i];
         }
     }
 }
@@ -536,15 +559,16 @@ static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, i
 template <int R, bool TILED>
 static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk,
                        int bps, int nsplit, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-    if (dec_waves() == 8) {
-        dim3 grid((tg.grp_end + 7) / 8, nsplit);
-        SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8>), grid, dim3(512), 0, s, tg, (const uint4*)a.frag, out, ldo,
-                  ss, nblk, bps);
+    const int W = dec_waves();
+    const dim3 grid((tg.grp_end + W - 1) / W, nsplit);
+    const uint4* fr = (const uint4*)a.frag;
+    if (a.rows_pad == 32) {
+        if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 2>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps);
+        else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 2>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps);
         return;
     }
-    dim3 grid((tg.grp_end + 3) / 4, nsplit);
-    SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED>), grid, dim3(256), 0, s, tg, (const uint4*)a.frag, out, ldo, ss,
-              nblk, bps);
+    if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 1>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps);
+    else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 1>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps);
 }
 
 constexpr int PF_R = 2, PF_WAVES = 8;
@@ -579,7 +603,9 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
     if (!a.frag || a.rows_pad < 16 || a.rows_pad % 16) { set_error(-1, "q4k: bad operand buffer"); return -1; }
     if (max_splits < 1) max_splits = 1;
     const int act_tiles = a.rows_pad / 16;
-    if (act_tiles > 1) {
+    // up to 32 rows: the decode kernel with one or two activation tiles
+    // (SLATE_HIP_Q4K_DEC32=0 sends 17..32 rows to the prompt kernel)
+    if (act_tiles > 2 || (act_tiles == 2 && !knobs().q4k_dec32)) {
         // the prompt kernel addresses the operand with 32-bit byte offsets
         if ((double)act_tiles * nblk * ACT_FRAG_UNITS * 16.0 >= 4294967296.0) {
             set_error(-1, "q4k: activation operand of %d rows x K=%d exceeds 4 GiB", a.rows_pad, a.K);

@@ -564,8 +564,20 @@ SWITCHES = [("SLATE_HIP_FUSED_NORM", "0", "q4k"), ("SLATE_HIP_ATTN_TOKENWISE", "
             ("SLATE_HIP_ATTN_ROPE", "2", "q4k"), ("SLATE_HIP_GRAPHS", "1", "q4k"),
             ("SLATE_HIP_Q4K_R", "1", "q4k"), ("SLATE_HIP_Q4K_R", "4", "q4k"), ("SLATE_HIP_Q4K_W", "4", "q4k"),
             ("SLATE_HIP_Q4K_S", "1", "q4k"), ("SLATE_HIP_Q4K_S", "3", "q4k"), ("SLATE_HIP_Q4K_WGS", "64", "q4k"),
-            ("SLATE_HIP_Q4K_PF_S", "3", "q4k"), ("SLATE_HIP_Q8_R", "1", "q8_0"), ("SLATE_HIP_Q8_R", "4", "q8_0"),
+            ("SLATE_HIP_Q4K_PF_S", "3", "q4k"), ("SLATE_HIP_Q4K_DEC32", "0", "q4k"),
+            ("SLATE_HIP_Q8_R", "1", "q8_0"), ("SLATE_HIP_Q8_R", "4", "q8_0"),
             ("SLATE_HIP_Q8_S", "2", "q8_0"), ("SLATE_HIP_Q8_WGS", "64", "q8_0")]
+
+
+def test_decode_steps_of_17_to_32_sequences(orc):
+    """Ragged decode steps of 24 sequences (32 padded rows: the Q4_K decode
+    kernel with two 16-row activation tiles, as the 70B workload's batches of
+    up to 32 run), after a prompt step, against the oracle."""
+    t = make_llama(FUSE, 4321, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(24)
+    prompts = [rng.integers(0, FUSE.vocab, n).astype(np.int32) for n in rng.integers(1, 9, 24)]
+    m = slate_amd.Llama.from_tensors(FUSE, t, max_slots=24, max_tokens=224)
+    replay_against_oracle(orc, FUSE, t, m, prompts, 3)
 
 
 @pytest.fixture

@@ -93,8 +93,9 @@ def test_matmul_q4k(hip, orc, M, K, B):
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336)])
 def test_matmul_q4k_c2_shapes(hip, orc, M, K):
     """The Q4_K op at its full sizes: W ~ N(0, 0.02) quantised to Q4_K on the
-    device, X ~ N(0, 1), B in {1, 4, 16, 64} (the small-batch GEMV, the
-    one-tile decode kernel and the prompt kernel), in slate's row layout and
+    device, X ~ N(0, 1), B in {1, 4, 16, 32, 64} (the one-row GEMV, the
+    decode kernel with one and two 16-row activation tiles and the prompt
+    kernel), in slate's row layout and
     the tiled layout, against the oracle's slate_q4_k_matvec
     (quant.c:306-313) and float64."""
     rng = np.random.default_rng(M + 3 * K)
@@ -105,7 +106,7 @@ def test_matmul_q4k_c2_shapes(hip, orc, M, K):
     T = DB(hip.lib.slate_hip_q4k_tiled_bytes(M, K))
     check(hip.lib.slate_hip_q4k_tile(T.p, Wd.p, M, K), "q4k_tile")
     deq = orc.dequant_q4k(raw, M * K).reshape(M, K).astype(np.float64)
-    for B in (1, 4, 16, 64):
+    for B in (1, 4, 16, 32, 64):
         X = rng.normal(0, 1, (B, K)).astype(np.float32)
         Xd = dev(X)
         Yr, Yt = DB(B * M * 4), DB(B * M * 4)
@@ -121,10 +122,11 @@ def test_matmul_q4k_c2_shapes(hip, orc, M, K):
 @pytest.mark.parametrize("M,K", [(1, 256), (37, 256), (100, 16640), (257, 2304)])
 @pytest.mark.parametrize("B", [1, 2, 3, 4])
 def test_matmul_q4k_small_batch_edges(hip, orc, M, K, B):
-    """The small-batch GEMV at its edges: one super-block (a single wave with
-    8 busy lanes), row counts that leave a partial workgroup, K above 64
-    super-blocks (two passes) and K not a multiple of 2048; row and tiled
-    layouts bit for bit, against the oracle."""
+    """Small batches at the edges of the kernels' tilings: one super-block
+    (in the one-row GEMV a single wave with 8 busy lanes), row counts that
+    leave a partial workgroup, K above 64 super-blocks (two GEMV passes) and
+    K not a multiple of 2048; row and tiled layouts bit for bit, against
+    the oracle."""
     rng = np.random.default_rng(M * 13 + K + B)
     raw = np.frombuffer(quantize_q4k(rng.normal(0, 0.02, (M, K)).astype(np.float32)), np.uint8).copy()
     X = rng.normal(0, 1, (B, K)).astype(np.float32)
