@@ -125,6 +125,16 @@ int   slate_hip_dequant_q4k(float* dst, const void* A_q4k, int64_t n);
 int64_t slate_hip_q4k_tiled_bytes(int M, int K);
 int   slate_hip_q4k_tile(void* dst_tiled, const void* src_q4k, int M, int K);
 int   slate_hip_matmul_q4k_tiled(float* Y, const void* A_tiled, const float* X, int B, int M, int K);
+/* slate_hip_matmul_q4k that allocates nothing, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid it); no counterpart in slate.  Same inputs,
+ * outputs and results; the activation operand and split-K partials live in
+ * a fixed 32 MiB device array of the library, so calls whose operand plus
+ * one split of partials ((16-row-padded B) * M * 4 bytes) exceed it return
+ * -1 with an error naming the limit.  Calls are serialised on the backend
+ * stream; work on that array from another stream (a replay of a captured
+ * call next to new calls, say) would race with it. */
+int   slate_hip_matmul_q4k_noalloc(float* Y, const void* A_q4k, const float* X, int B, int M, int K);
 /* Q8_0 (34-byte blocks [f16 d][32 x int8], quant.h:16-31), device pointers.
  * q8_0_matvec has slate_q8_0_matvec's signature and meaning (quant.c:126-133,
  * y[m] = sum_k d*q[m,k] * x[k], K % 32 == 0); matmul_q8_0 is B such calls in

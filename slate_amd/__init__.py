@@ -79,6 +79,7 @@ SIGNATURES = {
     "slate_hip_q4k_tiled_bytes": (C.c_int64, [C.c_int, C.c_int]),
     "slate_hip_q4k_tile": (C.c_int, [vp, vp, C.c_int, C.c_int]),
     "slate_hip_matmul_q4k_tiled": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int]),
+    "slate_hip_matmul_q4k_noalloc": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int]),
     "slate_hip_q8_0_matvec": (None, [vp, vp, vp, C.c_int, C.c_int]),
     "slate_hip_matmul_q8_0": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int]),
     "slate_hip_dequant_q8_0": (C.c_int, [vp, vp, C.c_int64]),

@@ -50,6 +50,15 @@ static int g_device = -1;
 static hipStream_t g_stream = nullptr;
 static bool g_ok = false;
 
+// Device scratch of slate_hip_matmul_q4k_noalloc: the activation operand and
+// the split-K partials of one call live here instead of in allocations.  In
+// host code the array's name is only a stand-in for its device copy: every
+// use goes through g_noalloc_scratch, the device address that
+// hipGetSymbolAddress returns at initialisation (one device per process).
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
+static __device__ __align__(256) unsigned char noalloc_scratch[NOALLOC_SCRATCH_BYTES];
+static void* g_noalloc_scratch = nullptr;
+
 static void init_device() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
@@ -68,6 +77,13 @@ static void init_device() {
     if (hipSetDevice(g_device) != hipSuccess ||
         hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) {
         set_error(-7, "cannot open device %d", g_device);
+        return;
+    }
+    // with the backend device current: its copy of the no-allocation scratch
+    const hipError_t es = hipGetSymbolAddress(&g_noalloc_scratch, HIP_SYMBOL(noalloc_scratch));
+    if (es != hipSuccess) {
+        g_noalloc_scratch = nullptr;
+        set_error(-7, "no-allocation scratch unavailable: %s", hipGetErrorString(es));
         return;
     }
     g_ok = true;
@@ -274,6 +290,38 @@ int slate_hip_matmul_q4k(float* Y, const void* A, const float* X, int B, int M, 
 
 int slate_hip_matmul_q4k_tiled(float* Y, const void* A, const float* X, int B, int M, int K) {
     return matmul_q4k_common(Y, A, X, B, M, K, true);
+}
+
+int slate_hip_matmul_q4k_noalloc(float* Y, const void* A, const float* X, int B, int M, int K) {
+    if (!ensure()) return -7;
+    SH_REQUIRE(Y && A && X && B > 0 && M > 0 && K > 0, "matmul_q4k_noalloc: bad arguments");
+    SH_REQUIRE(K % QK == 0, "matmul_q4k_noalloc: K=%d is not a multiple of 256", K);
+    std::lock_guard<std::mutex> lk(g_enqueue_mu);
+    Q4kTarget t{A, M, 0};
+    if (B <= GEMV_ROUTE_ROWS && ((uintptr_t)X & 15) == 0)   // needs no scratch
+        return launch_q4k_gemv(&t, 1, false, X, K, B, K, Y, M, g_stream);
+    Act16 a;
+    a.rows = B;
+    a.rows_pad = row_pad(B);
+    a.K = K;
+    const size_t act_bytes = (act_frag_bytes(a.rows_pad, K) + 255) & ~size_t(255);
+    const size_t split_bytes = (size_t)a.rows_pad * M * sizeof(float);
+    if (act_bytes + split_bytes > NOALLOC_SCRATCH_BYTES) {
+        set_error(-1, "matmul_q4k_noalloc: B=%d, M=%d, K=%d needs %zu bytes of scratch, above the %zu-byte limit",
+                  B, M, K, act_bytes + split_bytes, NOALLOC_SCRATCH_BYTES);
+        return -1;
+    }
+    // every split writes all of its partials and the operand covers every
+    // padded row, so nothing left by an earlier call is read
+    a.frag = g_noalloc_scratch;
+    float* part = (float*)((char*)g_noalloc_scratch + act_bytes);
+    const int max_splits = (int)std::min<size_t>(32, (NOALLOC_SCRATCH_BYTES - act_bytes) / split_bytes);
+    int rc = launch_act16_from_f32(a, X, K, g_stream);
+    if (rc) return rc;
+    int S = 1;
+    rc = launch_q4k(&t, 1, false, a, part, (int64_t)M, (int64_t)a.rows_pad * M, max_splits, &S, g_stream);
+    if (rc) return rc;
+    return launch_sum_splits(Y, part, S, B, a.rows_pad, M, g_stream);
 }
 
 int64_t slate_hip_q4k_tiled_bytes(int M, int K) {
