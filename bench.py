@@ -35,9 +35,10 @@ time) beside the nominal 8 TB/s.
 shapes (80 layers, d_model 8192, 64 Q / 8 KV heads, SwiGLU 28672, vocab
 128256, Q4_K), requests arriving as a Poisson process at 4 per second of
 wall time, prompts U[256, 4096], outputs U[64, 512], greedy, at most 32 in
-flight; prompts are prefilled in chunks inside the ragged steps next to the
-decode rows.  value = generated tokens / wall time over --duration seconds
-after --warmup-s seconds.
+flight; prompts are prefilled in chunks of at most --prefill-chunk tokens
+per step inside the ragged steps next to the decode rows (so the decode rows
+keep stepping while prompts stream in).  value = generated tokens / wall
+time over --duration seconds after --warmup-s seconds.
 
 --ops instead prints the op-level figures (one JSON object): the Q4_K and
 Q8_0 matmuls through the C ABI (pre-tiled weights) at (M, K) in {(4096, 4096), (14336, 4096), (4096, 14336)}
@@ -270,10 +271,11 @@ class PoissonWorkload:
     the ragged steps (the step's token budget minus its decode rows) and
     then decode until their output length."""
 
-    def __init__(self, m, shape, max_batch, rate, seed, max_tokens, prompt=(256, 4096), out=(64, 512)):
+    def __init__(self, m, shape, max_batch, rate, seed, max_tokens, prefill_chunk, prompt=(256, 4096), out=(64, 512)):
         self.m, self.shape, self.max_batch, self.rate = m, shape, max_batch, rate
         self.rng = np.random.default_rng(seed)
         self.max_tokens, self.prompt_rng, self.out_rng = max_tokens, prompt, out
+        self.prefill_chunk = prefill_chunk
         self.queue, self.active = [], []
         self.next_arrival = float(self.rng.exponential(1.0 / rate))
         self.arrived = self.completed = self.generated = 0
@@ -296,7 +298,8 @@ class PoissonWorkload:
         self.admit(now)
         if not self.active:
             return 0, False
-        budget = self.max_tokens - sum(1 for r in self.active if r["done"] == len(r["prompt"]))
+        n_dec = sum(1 for r in self.active if r["done"] == len(r["prompt"]))
+        budget = min(self.prefill_chunk, self.max_tokens - n_dec)
         rows, n_new, toks = [], [], []
         for r in self.active:
             left = len(r["prompt"]) - r["done"]
@@ -321,10 +324,11 @@ class PoissonWorkload:
             r["last"] = int(t)
             r["gen"] += 1
             gen += 1
-        for r in [r for r in self.active if r["gen"] >= r["out"]]:
+        done = [r for r in self.active if r["gen"] >= r["out"]]
+        for r in done:
             r["sess"].free()
-            self.active.remove(r)
-            self.completed += 1
+        self.active = [r for r in self.active if r["gen"] < r["out"]]
+        self.completed += len(done)
         self.generated += gen
         return gen, True
 
@@ -335,7 +339,7 @@ def run_c5(args, shape):
     t0 = time.perf_counter()
     m = slate_amd.Llama.synthetic(shape, seed=args.seed, quant=18, max_slots=max_batch, max_tokens=max_tokens)
     log(f"synthetic 70B-shape Q4_K model on device in {time.perf_counter() - t0:.1f} s")
-    wl = PoissonWorkload(m, shape, max_batch, rate, args.seed + 1, max_tokens)
+    wl = PoissonWorkload(m, shape, max_batch, rate, args.seed + 1, max_tokens, args.prefill_chunk)
     lib = slate_amd.load_library()
     start = time.perf_counter()
     now = 0.0
@@ -364,7 +368,7 @@ def run_c5(args, shape):
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "LLaMA-3-70B-shaped Q4_K serving: Poisson arrivals at 4 req/s, prompts "
                                "U[256,4096], outputs U[64,512], greedy, at most 32 in flight, prompts "
-                               "chunked into the ragged steps (4096-token budget)",
+                               f"chunked into the ragged steps ({args.prefill_chunk} prompt tokens per step)",
                    "layers": shape.n_layers, "d_model": shape.d_model,
                    "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "q4_k", "max_batch": max_batch, "arrivals": wl.arrived - a0,
@@ -385,6 +389,8 @@ def main():
                     help="8b (the headline line) or 70b (the 70B serving workload)")
     ap.add_argument("--duration", type=float, default=60.0, help="70b: timed seconds")
     ap.add_argument("--warmup-s", type=float, default=20.0, help="70b: untimed seconds from an empty system")
+    ap.add_argument("--prefill-chunk", type=int, default=384,
+                    help="70b: prompt tokens carried per step next to the decode rows (chunked prefill)")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference baseline")
     ap.add_argument("--copy-calibration", action="store_true",

@@ -92,6 +92,15 @@ typedef struct slate_hip_backend {
 
 /* NULL when no gfx950 device can be opened (like the reference's stubs). */
 const slate_backend_t* slate_backend_hip(void);                 /* replaces backend_cuda_stub.c:33 */
+/* The same kernels behind host-visible memory, for callers that treat the
+ * backend's memory as host memory (slate's toy engine memcpy's into its KV
+ * cache and passes module weights from host memory, src/infer/engine.c:
+ * 276-277, 411-412, 586-591): alloc returns pinned host memory the device
+ * reads directly, compute entries copy pageable arguments through device
+ * buffers and return after their kernel has finished.  Correct, slow; for
+ * running slate_infer_engine_new_ex (infer.h:90-96) unchanged.  NULL
+ * without a gfx950 device. */
+const slate_backend_t* slate_backend_hip_compat(void);
 
 /* ---- errors -------------------------------------------------------------- */
 const char* slate_hip_last_error(void);  /* NULL when no error is pending */

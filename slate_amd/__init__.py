@@ -58,6 +58,7 @@ class LlamaLayer(C.Structure):          # slate_hip_llama_layer_t == llama.h:69-
 # name -> (restype, argtypes) for every exported entry point
 SIGNATURES = {
     "slate_backend_hip": (C.POINTER(BackendStruct), []),
+    "slate_backend_hip_compat": (C.POINTER(BackendStruct), []),
     "slate_hip_last_error": (C.c_char_p, []),
     "slate_hip_clear_error": (None, []),
     "slate_hip_stream": (vp, []),

@@ -572,3 +572,183 @@ const slate_backend_t* slate_backend_hip(void) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Compatibility vtable (slate_backend_hip_compat): the same kernels for
+// callers that treat backend memory as host memory, like slate's toy engine
+// (src/infer/engine.c memcpy's and memset's its KV cache, engine.c:411-412,
+// 586-591, and hands module weights, which live in ordinary host memory,
+// straight to the compute entries).  alloc returns pinned host memory that
+// the device addresses directly; a compute entry runs its kernel on device
+// views of its arguments -- device and pinned memory as they are, any
+// other (pageable) host range copied into a temporary device buffer and,
+// for outputs, back -- and waits for the kernel before returning, since
+// such callers read the results at once.  Correct and slow.
+
+namespace {
+
+struct CompatArg { const void* host; void* dev; size_t bytes; bool out; bool own; };
+
+class CompatCall {
+  public:
+    ~CompatCall() { finish(); }
+    // A device view of [p, p + bytes) for a kernel argument read (in)
+    // and/or written (out); the same pointer passed twice gets one view.
+    template <class T>
+    T* arg(T* p, size_t bytes, bool in, bool out) {
+        if (!p || !ok_) return p;
+        for (auto& a : args_)
+            if (a.host == (const void*)p) {
+                a.out = a.out || out;
+                return (T*)a.dev;
+            }
+        hipPointerAttribute_t at{};
+        if (hipPointerGetAttributes(&at, (const void*)p) == hipSuccess &&
+            (at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeHost) && at.devicePointer) {
+            args_.push_back({(const void*)p, at.devicePointer, bytes, false, false});
+            return (T*)at.devicePointer;
+        }
+        (void)hipGetLastError();   // an unregistered pointer is not an error here
+        void* d = nullptr;
+        if (hipMalloc(&d, bytes ? bytes : 1) != hipSuccess ||
+            (in && bytes && hipMemcpy(d, (const void*)p, bytes, hipMemcpyHostToDevice) != hipSuccess)) {
+            if (d) (void)hipFree(d);
+            set_error(-7, "compat backend: staging %zu bytes failed", bytes);
+            ok_ = false;
+            return nullptr;
+        }
+        args_.push_back({(const void*)p, d, bytes, out, true});
+        return (T*)d;
+    }
+    bool ok() const { return ok_; }
+    // wait for the kernels, copy staged outputs back, free the staging
+    void finish() {
+        if (done_) return;
+        done_ = true;
+        if (hipStreamSynchronize(stream()) != hipSuccess) set_error(-7, "compat backend: kernel failed");
+        for (auto& a : args_) {
+            if (!a.own) continue;
+            if (ok_ && a.out && a.bytes &&
+                hipMemcpy((void*)a.host, a.dev, a.bytes, hipMemcpyDeviceToHost) != hipSuccess)
+                set_error(-7, "compat backend: copy back of %zu bytes failed", a.bytes);
+            (void)hipFree(a.dev);
+        }
+    }
+
+  private:
+    std::vector<CompatArg> args_;
+    bool ok_ = true, done_ = false;
+};
+
+void* compat_alloc(size_t bytes) {
+    if (!bytes || !ensure()) return nullptr;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+        set_error(-2, "compat alloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+
+void compat_release(void* p) {
+    if (!p || !ensure()) return;
+    (void)hipStreamSynchronize(stream());
+    if (hipHostFree(p) != hipSuccess) set_error(-7, "compat release(%p) failed", p);
+}
+
+void compat_copy(void* dst, const void* src, size_t bytes) {
+    if (!bytes || !ensure()) return;
+    (void)hipStreamSynchronize(stream());
+    if (hipMemcpy(dst, src, bytes, hipMemcpyDefault) != hipSuccess) set_error(-7, "compat copy(%zu) failed", bytes);
+}
+
+void compat_matvec(float* y, const float* A, const float* x, int M, int K) {
+    if (!ensure() || M <= 0 || K <= 0) { slate_hip_matvec(y, A, x, M, K); return; }
+    CompatCall c;
+    float* dy = c.arg(y, (size_t)M * 4, false, true);
+    const float* dA = c.arg(A, (size_t)M * K * 4, true, false);
+    const float* dx = c.arg(x, (size_t)K * 4, true, false);
+    if (c.ok()) slate_hip_matvec(dy, dA, dx, M, K);
+}
+
+void compat_linear_batch(float* C, const float* X, const float* W, int B, int K, int N) {
+    if (!ensure() || B <= 0 || K <= 0 || N <= 0) { slate_hip_linear_batch(C, X, W, B, K, N); return; }
+    CompatCall c;
+    float* dC = c.arg(C, (size_t)B * N * 4, false, true);
+    const float* dX = c.arg(X, (size_t)B * K * 4, true, false);
+    const float* dW = c.arg(W, (size_t)K * N * 4, true, false);
+    if (c.ok()) slate_hip_linear_batch(dC, dX, dW, B, K, N);
+}
+
+void compat_matvec_q4k(float* y, const void* A, const float* x, int M, int K) {
+    if (!ensure() || M <= 0 || K <= 0 || K % QK) { slate_hip_matvec_q4k(y, A, x, M, K); return; }
+    CompatCall c;
+    float* dy = c.arg(y, (size_t)M * 4, false, true);
+    const void* dA = c.arg(A, (size_t)M * (K / QK) * QBLOCK, true, false);
+    const float* dx = c.arg(x, (size_t)K * 4, true, false);
+    if (c.ok()) slate_hip_matvec_q4k(dy, dA, dx, M, K);
+}
+
+void compat_rmsnorm_row(float* y, const float* x, const float* w, int D, float eps) {
+    if (!ensure() || D <= 0) { slate_hip_rmsnorm_row(y, x, w, D, eps); return; }
+    CompatCall c;
+    float* dy = c.arg(y, (size_t)D * 4, false, true);
+    const float* dx = c.arg(x, (size_t)D * 4, true, false);
+    const float* dw = c.arg(w, (size_t)D * 4, true, false);
+    if (c.ok()) slate_hip_rmsnorm_row(dy, dx, dw, D, eps);
+}
+
+void compat_silu_mul(float* y, const float* gate, const float* up, int H) {
+    if (!ensure() || H <= 0) { slate_hip_silu_mul(y, gate, up, H); return; }
+    CompatCall c;   // y == gate (in place, llama_infer.c:192) shares one view
+    const float* dg = c.arg(gate, (size_t)H * 4, true, false);
+    const float* du = c.arg(up, (size_t)H * 4, true, false);
+    float* dy = c.arg(y, (size_t)H * 4, false, true);
+    if (c.ok()) slate_hip_silu_mul(dy, dg, du, H);
+}
+
+void compat_add_inplace(float* y, const float* x, int D) {
+    if (!ensure() || D <= 0) { slate_hip_add_inplace(y, x, D); return; }
+    CompatCall c;
+    float* dy = c.arg(y, (size_t)D * 4, true, true);
+    const float* dx = c.arg(x, (size_t)D * 4, true, false);
+    if (c.ok()) slate_hip_add_inplace(dy, dx, D);
+}
+
+void compat_embed_lookup(float* y, const float* W, int token_id, int D) {
+    if (!ensure() || !W || token_id < 0 || D <= 0) { slate_hip_embed_lookup(y, W, token_id, D); return; }
+    CompatCall c;   // only the looked-up row of the table is staged
+    float* dy = c.arg(y, (size_t)D * 4, false, true);
+    const float* dW = c.arg(W + (int64_t)token_id * D, (size_t)D * 4, true, false);
+    if (c.ok()) slate_hip_embed_lookup(dy, dW, 0, D);
+}
+
+void compat_attention_step(float* out, const float* q, const float* K, const float* V, float* scores, int L,
+                           int D) {
+    if (!ensure() || L <= 0 || D <= 0) { slate_hip_attention_step(out, q, K, V, scores, L, D); return; }
+    CompatCall c;
+    float* dout = c.arg(out, (size_t)D * 4, false, true);
+    const float* dq = c.arg(q, (size_t)D * 4, true, false);
+    const float* dK = c.arg(K, (size_t)L * D * 4, true, false);
+    const float* dV = c.arg(V, (size_t)L * D * 4, true, false);
+    float* ds = c.arg(scores, (size_t)L * 4, false, true);
+    if (c.ok()) slate_hip_attention_step(dout, dq, dK, dV, ds, L, D);
+}
+
+const slate_backend_t g_compat = {
+    "hip-compat",      compat_alloc,       compat_release,      compat_copy,
+    compat_copy,       compat_matvec,      compat_linear_batch, compat_matvec_q4k,
+    compat_rmsnorm_row, compat_silu_mul,   compat_add_inplace,  compat_embed_lookup,
+    compat_attention_step, slate_hip_sync,
+};
+
+}  // namespace
+
+extern "C" {
+
+const slate_backend_t* slate_backend_hip_compat(void) {
+    if (!ensure()) return nullptr;
+    return &g_compat;
+}
+
+}  // extern "C"

@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "slate_hip.h")
 def declared_functions():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    names = set(re.findall(r"\b(slate_(?:hip_\w+|backend_hip))\s*\(", src))
+    names = set(re.findall(r"\b(slate_(?:hip_\w+|backend_hip\w*))\s*\(", src))
     # drop struct members written as (*name)(...)
     return sorted(n for n in names if not re.search(r"\(\*\s*" + n + r"\)", src))
 

@@ -85,3 +85,38 @@ def test_binding_library_exports_the_binding():
         pytest.skip("oracle/_ref not built")
     out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True, check=True).stdout
     assert re.search(r" T slate_llama_to_hip$", out, flags=re.M)
+
+
+INFER_API = ["slate_infer_engine_free", "slate_infer_engine_vocab", "slate_infer_engine_max_seq",
+             "slate_infer_session_new", "slate_infer_session_free", "slate_infer_session_reset",
+             "slate_infer_session_position", "slate_infer_prefill", "slate_infer_decode_step",
+             "slate_infer_batch_new", "slate_infer_batch_free", "slate_infer_batch_step"]
+
+
+def test_infer_library_exports_slate_infer_api():
+    """libslate_hip_infer.so defines every infer.h entry a LLaMA caller uses
+    (all but the slate_module_t constructors, infer.h:74-96) plus its own
+    constructor; it is linked with --no-undefined."""
+    so = os.path.join(ROOT, "slate_amd", "libslate_hip_infer.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert set(INFER_API) | {"slate_hip_infer_engine_new"} <= exported
+    api = open(os.path.join(REF_INCLUDE, "slate", "infer.h")).read()
+    declared = set(re.findall(r"\b(slate_infer_\w+)\s*\(", api))
+    assert declared - set(INFER_API) == {"slate_infer_engine_new", "slate_infer_engine_new_ex"}
+
+
+def test_infer_headers_compile_together(tmp_path):
+    """slate's infer.h and slate_hip_infer.h declare the same opaque types,
+    so a caller such as scheduler.c can use both (in C: slate's runtime.h,
+    which infer.h includes, is not valid C++)."""
+    src = ('#include "slate/infer.h"\n#include "slate_hip_infer.h"\n'
+           "int run(slate_hip_llama_t* m, const int32_t* t, float* lg) {\n"
+           "    slate_infer_engine_t* e = slate_hip_infer_engine_new(m);\n"
+           "    slate_infer_batch_t* b = slate_infer_batch_new(e, 4);\n"
+           "    slate_infer_session_t* s = slate_infer_session_new(e);\n"
+           "    int rc = slate_infer_batch_step(b, &s, 1, t, lg);\n"
+           "    slate_infer_session_free(s); slate_infer_batch_free(b); slate_infer_engine_free(e);\n"
+           "    return rc;\n}\n")
+    rc, err = compile_c(tmp_path, src)
+    assert rc == 0, err
