@@ -79,6 +79,8 @@ struct slate_hip_llama {
     float* ssq = nullptr;          // [T_pad][D/256] block sums of squares (deferred RMSNorm)
     bool defer_norm = true;
     bool tokenwise_attn = false;   // prompt-chunk tokens through the decode attention kernel
+    bool prompt_mfma = false;      // prompt-chunk blocks may go to the MFMA prompt attention kernel
+    bool step_prompt_mfma = false; // ... and do in the step being enqueued
     float *att_po = nullptr, *att_pml = nullptr;
     Act16 act{};
     Act8 act8{};                   // allocated with the first Q8_0 linear
@@ -208,7 +210,10 @@ int alloc_runtime(slate_hip_llama* m) {
     m->graphs_on = getenv("SLATE_HIP_GRAPHS") != nullptr && atoi(getenv("SLATE_HIP_GRAPHS")) != 0;
     // prompt-chunk tokens attend through the decode kernel (one query token
     // per work unit, whole coalesced K/V rows; the shared prefix re-reads
-    // hit L2), which beats the query-block kernel for these head sizes
+    // hit L2), which beats the query-block kernel for these head sizes; the
+    // MFMA prompt kernel, where it covers the shape, takes them in steps where
+    // it pays (prompt_mfma_pays)
+    m->prompt_mfma = attention_prompt_mfma(c.n_heads, c.n_kv_heads, c.head_dim, m->kv_f16);
     m->tokenwise_attn = (c.head_dim == 32 || c.head_dim == 64 || c.head_dim == 128) &&
                         (m->kv_f16 || getenv("SLATE_HIP_ATTN_TOKENWISE") == nullptr ||
                          atoi(getenv("SLATE_HIP_ATTN_TOKENWISE")) != 0);
@@ -575,7 +580,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                                                   m->n_dec, d_blk + m->n_dec, d_blk + m->n_dec + m->n_pre, m->n_pre,
                                                   c.n_heads, c.n_kv_heads, hd, m->head_stride, c.max_seq, m->att_po,
                                                   m->att_pml, gi.q4 ? &a : nullptr, s, prof_ev(m, ea),
-                                                  prof_ev(m, eb), true, m->kv_f16)))
+                                                  prof_ev(m, eb), true, m->kv_f16, m->step_prompt_mfma)))
                     return rc;
             }
             if (m->prof_on)   // K and V once per kv head per sequence, q in and out once
@@ -667,6 +672,30 @@ int capture_step(slate_hip_llama* m, int n, int T, bool want, hipStream_t s, hip
         return -7;
     }
     return 0;
+}
+
+// Whether a step's prompt chunks should attend on the MFMA prompt kernel
+// rather than with its decode tokens in the tokenwise decode kernel.  The
+// tokenwise launch overlaps prompt work with the decode tokens' K/V streaming
+// (HBM-bound), the MFMA kernel runs after them: it pays when the prompt
+// attention flops (4 per q head, key and element) reach about 6 per decode
+// K/V byte (measured on MI355X at the 8B shape: a 200-token chunk at
+// position 300 beside 15 decode tokens at ~1200 context, ratio 7.8, takes
+// 61 us on the MFMA kernel and 68 us tokenwise; a 100-token chunk at 0,
+// ratio 0.5, 45 and 37 us).  Steps without decode tokens always take it.
+bool prompt_mfma_pays(const slate_hip_llama* m, slate_hip_llama_session_t* const* sessions, int n,
+                      const int32_t* n_new) {
+    if (knobs().attn_mfma == 2) return true;
+    const auto& c = m->cfg;
+    double prompt_keys = 0, decode_keys = 0;   // (query token, key) pairs
+    for (int i = 0; i < n; ++i) {
+        const double p0 = sessions[i]->pos, k = n_new[i];
+        if (k > 1) prompt_keys += k * p0 + k * (k + 1) / 2;
+        else decode_keys += p0 + 1;
+    }
+    const double flops = prompt_keys * c.n_heads * c.head_dim * 4.0;
+    const double bytes = decode_keys * c.n_kv_heads * c.head_dim * 8.0;
+    return flops >= 6.0 * bytes;
 }
 
 int new_common(slate_hip_llama* m, const slate_hip_llama_config_t* cfg, int max_slots, int max_tokens) {
@@ -954,16 +983,20 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
     // attention work: decode tokens one per block, prompt chunks in blocks of
     // consecutive tokens of one sequence (or one block per token, tokenwise)
     {
-        const int QB = attn_prefill_block(c.n_heads / c.n_kv_heads);
+        const bool mfma = m->prompt_mfma && prompt_mfma_pays(m, sessions, n, n_new);
+        const bool tokenwise = !mfma && m->tokenwise_attn;
+        const int G = c.n_heads / c.n_kv_heads;
+        const int QB = mfma ? attention_prompt_block(G) : attn_prefill_block(G);
         int32_t* blk = m->h_tok + T;
         int nd = 0, np = 0, t = 0;
         for (int i = 0; i < n; ++i) {
-            if (n_new[i] == 1 || m->tokenwise_attn) nd += n_new[i];
+            if (n_new[i] == 1 || tokenwise) nd += n_new[i];
             else np += (n_new[i] + QB - 1) / QB;
         }
+        m->step_prompt_mfma = mfma && np > 0;
         int id = 0, ip = 0;
         for (int i = 0; i < n; ++i) {
-            if (n_new[i] == 1 || m->tokenwise_attn) {
+            if (n_new[i] == 1 || tokenwise) {
                 for (int k = 0; k < n_new[i]; ++k) blk[id++] = t + k;
             } else {
                 for (int k = 0; k < n_new[i]; k += QB) {

@@ -866,7 +866,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
                             hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool pairs_ready,
-                            bool kv_f16) {
+                            bool kv_f16, bool prompt_mfma) {
     if (T <= 0) return 0;
     if (kv_f16 && (n_pre > 0 || !(HD == 32 || HD == 64 || HD == 128))) {
         set_error(-5, "attention: f16 K/V caches need head_dim 32, 64 or 128 and one work unit per token");
@@ -897,7 +897,11 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
         a.qn = prefill ? pre_n : nullptr;
         dim3 grid(nch_max, nblk, Hkv);
         int rc;
-        if (!prefill && (HD == 32 || HD == 64 || HD == 128)) {
+        if (prefill && prompt_mfma) {
+            rc = launch_attention_prompt(q, (const float*)Kp, (const float*)Vp, tok2seq, tok_pos, kv_base, pre_t0,
+                                         pre_n, n_pre, Hq, Hkv, HD, head_stride, nch_max, po, pml, s, a.ev0);
+            if (rc) return rc;
+        } else if (!prefill && (HD == 32 || HD == 64 || HD == 128)) {
             if (!pairs_ready) {
                 SH_LAUNCH(a.ev0, nullptr, attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos,
                           tok2seq, kv_base, nch_max, pairs);

@@ -48,7 +48,10 @@ int launch_linear_batch(float* C, const float* X, const float* W, int B, int K, 
 int attn_chunk_size();
 int attn_prefill_block(int group);   // query tokens per block for prompt chunks
 // Blocks: dec_t0[n_dec] decode tokens (one each); pre_t0/pre_n[n_pre] runs of
-// consecutive tokens of one sequence.  Every token must be covered once.
+// consecutive tokens of one sequence, at most attn_prefill_block(G) tokens
+// each, or attention_prompt_block(G) with prompt_mfma (the MFMA prompt kernel,
+// for shapes where attention_prompt_mfma holds).  Every token must be covered
+// once.
 // `act` (nullable) also receives the output rows as the Q4_K activation
 // operand (Hq * HD % 256 == 0).
 int launch_attention_blocks(float* out, const float* q, const void* Kp, const void* Vp, const int32_t* tok2seq,
@@ -56,7 +59,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
                             int n_dec, const int32_t* pre_t0, const int32_t* pre_n, int n_pre, int Hq, int Hkv,
                             int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
                             hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr,
-                            bool pairs_ready = false, bool kv_f16 = false);
+                            bool pairs_ready = false, bool kv_f16 = false, bool prompt_mfma = false);
 // The decode work-unit list that launch_attention_blocks builds (in the tail
 // of the pml buffer) when pairs_ready is false: build it once when several
 // launches share the same tokens and positions (the layers of one step).
@@ -77,6 +80,18 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
                             float* pml, hipStream_t s);
 int launch_attention_step(float* out, const float* q, const float* K, const float* V, float* scores, int L,
                           int D, hipStream_t s);
+
+// k_attn_mfma.hip: prompt blocks (<= attention_prompt_block(G) consecutive
+// tokens of one sequence, G = Hq / Hkv) on MFMA, leaving partials in the
+// layout the merge kernel reads.  attention_prompt_mfma: the shape is one
+// the kernel covers (f32 K/V, head_dim 64 or 128, 1, 2, 4 or 8 q heads per
+// kv head) and SLATE_HIP_ATTN_MFMA is not 0.
+bool attention_prompt_mfma(int Hq, int Hkv, int HD, bool kv_f16);
+int attention_prompt_block(int G);
+int launch_attention_prompt(const float* q, const float* Kp, const float* Vp, const int32_t* tok2seq,
+                            const int32_t* tok_pos, const int64_t* kv_base, const int32_t* blk_t0,
+                            const int32_t* blk_n, int n_blk, int Hq, int Hkv, int HD, int64_t head_stride,
+                            int nch_max, float* po, float* pml, hipStream_t s, hipEvent_t ev0);
 
 // k_synth.hip
 int launch_synth_f32(float* dst, int64_t n, uint64_t seed, float std, float fill, hipStream_t s);

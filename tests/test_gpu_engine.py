@@ -318,11 +318,12 @@ def test_fused_rope_attention_head_groups(orc, d_model, n_heads, n_kv_heads):
             tok = int(np.argmax(steps[k][i]))
 
 
-def test_fused_rope_phased_attention_equals_separate_kernels():
+def test_fused_rope_phased_attention_equals_separate_kernels(switch_env):
     """As below for a head group too wide for the wave kernel (8 query heads of
     128 per kv head, as the 70B shape): the fused path runs in the phased
     kernel, the separate path in the same kernel without the prologue; K/V
     caches bit-identical, logits within 1e-5."""
+    switch_env.setenv("SLATE_HIP_ATTN_MFMA", "0")
     shape = LlamaShape(2, 2048, 16, 2, 768, 300, 512)
     rng = np.random.default_rng(22)
     prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (253, 30)]
@@ -334,7 +335,7 @@ def test_fused_rope_phased_attention_equals_separate_kernels():
         assert np.array_equal(Ka[:, :n], Kb[:, :n]) and np.array_equal(Va[:, :n], Vb[:, :n])
 
 
-def test_fused_rope_attention_equals_separate_kernels():
+def test_fused_rope_attention_equals_separate_kernels(switch_env):
     """Steps in which every sequence adds one token rotate q/k and append K/V
     inside the decode attention kernel; a step adding several tokens of a
     sequence runs RoPE/append and attention as separate kernels.  The same
@@ -344,7 +345,11 @@ def test_fused_rope_attention_equals_separate_kernels():
     bit-identical K/V caches (layer 1's rows carry layer 0's attention
     output): per token the two paths evaluate the same expressions.  The
     final logits agree within 1e-5: single-token steps also defer the final
-    RMSNorm factor to the argmax, the four-token step normalises the rows."""
+    RMSNorm factor to the argmax, the four-token step normalises the rows.
+    The four-token step's tokens attend tokenwise (SLATE_HIP_ATTN_MFMA=0), in
+    the decode kernel the fused path also runs; the MFMA prompt kernel rounds
+    differently and has its own tests."""
+    switch_env.setenv("SLATE_HIP_ATTN_MFMA", "0")
     shape = LlamaShape(2, 512, 8, 4, 768, 300, 512)
     rng = np.random.default_rng(21)
     prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (254, 40)]
@@ -559,7 +564,10 @@ def test_q4k_gate_up_with_unaligned_ffn_width(orc):
 # f16 K/V cache has its own tolerance study above).  Six sequences, so that
 # decode steps run the 16-row MFMA decode kernels the Q4_K / Q8_0 plan
 # switches steer; a 68-token prompt step for the prompt kernels.
-SWITCHES = [("SLATE_HIP_FUSED_NORM", "0", "q4k"), ("SLATE_HIP_ATTN_TOKENWISE", "0", "q4k"),
+SWITCHES = [("SLATE_HIP_FUSED_NORM", "0", "q4k"), ("SLATE_HIP_ATTN_MFMA", "0", "q4k"),
+            ("SLATE_HIP_ATTN_MFMA", "2", "q4k"),
+            # the query-block prompt kernel: neither the MFMA nor the tokenwise path
+            ("SLATE_HIP_ATTN_MFMA=0,SLATE_HIP_ATTN_TOKENWISE", "0", "q4k"),
             ("SLATE_HIP_ATTN_WAVE", "0", "q4k"), ("SLATE_HIP_ATTN_ROPE", "0", "q4k"),
             ("SLATE_HIP_ATTN_ROPE", "2", "q4k"), ("SLATE_HIP_GRAPHS", "1", "q4k"),
             ("SLATE_HIP_Q4K_R", "1", "q4k"), ("SLATE_HIP_Q4K_R", "4", "q4k"), ("SLATE_HIP_Q4K_W", "4", "q4k"),
@@ -592,7 +600,9 @@ def switch_env(monkeypatch):
 
 @pytest.mark.parametrize("name,value,quant", SWITCHES)
 def test_engine_switch_matches_oracle(orc, switch_env, name, value, quant):
-    switch_env.setenv(name, value)
+    for kv in name.split(",")[:-1]:                # leading NAME=VALUE settings
+        switch_env.setenv(*kv.split("="))
+    switch_env.setenv(name.split(",")[-1], value)
     t = make_llama(FUSE, 4321, quant=quant, output_quant=quant)
     rng = np.random.default_rng(12)
     prompts = [rng.integers(0, FUSE.vocab, n).astype(np.int32) for n in (40, 9, 3, 1, 12, 3)]
