@@ -511,6 +511,25 @@ def run_ops(seed):
             for c in range(ncopy):
                 slate_amd.check(tile(copies[c].data_ptr(), raw.data_ptr(), M, K), fmt + " tile")
             lib.slate_hip_sync()
+            if fmt == "q4k":
+                # one activation row on slate's own row layout (the vtable's
+                # matvec_q4k, backend.h:63-70): the one-kernel GEMV
+                rows = torch.empty((ncopy, nblk * qb), dtype=torch.uint8, device="cuda")
+                rows.copy_(raw.reshape(1, -1).expand(ncopy, -1))
+                X = torch.randn(1, K, device="cuda", generator=gen)
+                Y = torch.empty(1, M, device="cuda")
+                torch.cuda.synchronize()
+
+                def call_row(i, X=X, Y=Y):
+                    slate_amd.check(lib.slate_hip_matmul_q4k(Y.data_ptr(), rows[i % ncopy].data_ptr(),
+                                                             X.data_ptr(), 1, M, K), "q4k matmul (row layout)")
+                us, same = graph_time_us(call_row, 2 * ncopy, stream, Y)
+                alg = nblk * qb + 4 * K + 4 * M
+                out["q4k_row_B1"] = out.get("q4k_row_B1", []) + [
+                    {"M": M, "K": K, "B": 1, "layout": "row", "us": round(us, 2), "GBs": round(alg / us / 1e3, 1),
+                     "frac_hbm": round(alg / us / 1e3 / HBM_PEAK_GBS, 3), "replays_match_eager": same}]
+                log(fmt, out["q4k_row_B1"][-1])
+                del rows
             del raw
             for B in (1, 4, 16, 32, 64):
                 X = torch.randn(B, K, device="cuda", generator=gen)

@@ -1037,57 +1037,71 @@ int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_
 
 // ---------------------------------------------------------------------------
 // Single-head step of the vtable (backend_cpu.c:117-166), any D and L: one
-// workgroup; scores land in the caller's scratch `scores` [L] as there.
-__global__ __launch_bounds__(256) void attention_step_kernel(float* __restrict__ out,
-                                                             const float* __restrict__ q,
-                                                             const float* __restrict__ K,
-                                                             const float* __restrict__ V,
-                                                             float* __restrict__ scores, int L, int D) {
-    __shared__ float red[256];
-    __shared__ double redd[256];
-    const int tid = threadIdx.x;
+// workgroup of 16 waves.  Scores: one wave per key (lanes over d, coalesced
+// K rows, DPP sum); softmax with the reference's double sum, leaving the
+// probabilities in the caller's scratch `scores` [L] as there; then
+// out[d] = sum_t p_t V[t, d] with lanes over d and the waves' t-slices
+// combined in LDS in a fixed order (deterministic).  L <= 0 writes zeros.
+constexpr int ATT_STEP_THREADS = 1024;
+__global__ __launch_bounds__(ATT_STEP_THREADS) void attention_step_kernel(float* __restrict__ out,
+                                                                          const float* __restrict__ q,
+                                                                          const float* __restrict__ K,
+                                                                          const float* __restrict__ V,
+                                                                          float* __restrict__ scores, int L, int D) {
+    constexpr int NW = ATT_STEP_THREADS / 64;
+    __shared__ float red[ATT_STEP_THREADS];
+    __shared__ double redd[NW];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float scale = 1.0f / sqrtf((float)D);
     float mx = -INFINITY;
-    for (int t = tid; t < L; t += 256) {
+    for (int t = wv; t < L; t += NW) {
         const float* k = K + (size_t)t * D;
         float a = 0.f;
-        for (int d = 0; d < D; ++d) a = __builtin_fmaf(q[d], k[d], a);
-        float sc = a * scale;
-        scores[t] = sc;
+        for (int d = lane; d < D; d += 64) a = __builtin_fmaf(q[d], k[d], a);
+        const float sc = wave_sum(a) * scale;
+        if (lane == 0) scores[t] = sc;
         mx = fmaxf(mx, sc);
     }
-    red[tid] = mx;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) red[tid] = fmaxf(red[tid], red[tid + o]);
-        __syncthreads();
-    }
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();                               // also orders the scores stores
     mx = red[0];
+    for (int i = 1; i < NW; ++i) mx = fmaxf(mx, red[i]);
     double S = 0;
-    for (int t = tid; t < L; t += 256) {
-        float e = expf(scores[t] - mx);
+    for (int t = tid; t < L; t += ATT_STEP_THREADS) {
+        const float e = expf(scores[t] - mx);
         scores[t] = e;
         S += (double)e;
     }
-    redd[tid] = S;
+    for (int o = 32; o > 0; o >>= 1) S += __shfl_xor(S, o, 64);
+    if (lane == 0) redd[wv] = S;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (tid < o) redd[tid] += redd[tid + o];
-        __syncthreads();
-    }
-    float invS = (float)(1.0 / redd[0]);
-    for (int t = tid; t < L; t += 256) scores[t] *= invS;
+    S = 0;
+    for (int i = 0; i < NW; ++i) S += redd[i];
+    const float invS = (float)(1.0 / S);
+    for (int t = tid; t < L; t += ATT_STEP_THREADS) scores[t] *= invS;
     __syncthreads();
-    for (int d = tid; d < D; d += 256) {
+    // lanes over d (DL of them, whole waves), TS = threads / DL slices of t
+    for (int d0 = 0; d0 < D; d0 += ATT_STEP_THREADS) {
+        const int Dc = min(D - d0, ATT_STEP_THREADS);
+        const int DL = (Dc + 63) & ~63, TS = ATT_STEP_THREADS / DL;
+        const int dl = tid % DL, ts = tid / DL, d = d0 + dl;
         float acc = 0.f;
-        for (int t = 0; t < L; ++t) acc = __builtin_fmaf(scores[t], V[(size_t)t * D + d], acc);
-        out[d] = acc;
+        if (ts < TS && dl < Dc)
+            for (int t = ts; t < L; t += TS) acc = __builtin_fmaf(scores[t], V[(size_t)t * D + d], acc);
+        red[tid] = acc;
+        __syncthreads();
+        if (tid < Dc) {
+            float v = 0.f;
+            for (int i = 0; i < TS; ++i) v += red[i * DL + tid];
+            out[d0 + tid] = L > 0 ? v : 0.f;
+        }
+        __syncthreads();
     }
 }
 
 int launch_attention_step(float* out, const float* q, const float* K, const float* V, float* scores, int L,
                           int D, hipStream_t s) {
-    hipLaunchKernelGGL(attention_step_kernel, dim3(1), dim3(256), 0, s, out, q, K, V, scores, L, D);
+    hipLaunchKernelGGL(attention_step_kernel, dim3(1), dim3(ATT_STEP_THREADS), 0, s, out, q, K, V, scores, L, D);
     SH_CHECK_LAUNCH();
     return 0;
 }

@@ -31,6 +31,16 @@ namespace slate_hip {
 
 constexpr int GEMV_WAVES = 8;                  // 512 threads
 
+// x & m in inline assembly: the compiler cannot fold the mask into the byte
+// extractions that follow, so each masked byte becomes a float with one
+// v_cvt_f32_ubyte0..3 (folded, every nibble costs a field extract and a
+// conversion).
+__device__ __forceinline__ uint32_t and_opaque(uint32_t x, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(x));
+    return r;
+}
+
 // tg: up to three tensors sharing X; tensor i owns workgroups
 // [grp0[i], grp0[i+1]) of R rows each and writes Y columns [col, col + M).
 // X: nb rows (nb <= B) of K f32, ldx apart; Y: nb rows, ldy apart.
@@ -61,70 +71,73 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void q4k_gemv_kernel(Q4kTargets tg
         for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
 
     for (int kc = 0; kc < nblk; kc += nw * 8) {
+        // lanes past the last block read block nblk - 1 and weigh it by x = 0
         const int kb = kc + (t >> 3);
-        if (kb < nblk) {
-            uint4 hd[R], qv[R];
+        const bool live = kb < nblk;
+        const int kbc = live ? kb : nblk - 1;
+        float x[B][32], xs[B];
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int m = min(m0 + r, M - 1);
-                const uint8_t* hp;
-                const uint8_t* qp;
-                if (TILED) {
-                    const uint8_t* tb = W + ((size_t)(m >> 4) * nblk + kb) * (16 * QBLOCK);
-                    hp = tb + 16 * (m & 15);
-                    qp = tb + ((s & 1) ? 1280 : 256) + 16 * (16 * (s >> 1) + (m & 15));
-                } else {
-                    hp = W + ((size_t)m * nblk + kb) * QBLOCK;
-                    qp = hp + 16 + 16 * s;
-                }
-                hd[r] = *(const uint4*)hp;
-                qv[r] = *(const uint4*)qp;
+        for (int b = 0; b < B; ++b) {
+            const float4* xp = (const float4*)(X + (int64_t)min(b, nb - 1) * ldx + (int64_t)kbc * QK + 32 * s);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v = (b < nb && live) ? xp[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                x[b][4 * i] = v.x;
+                x[b][4 * i + 1] = v.y;
+                x[b][4 * i + 2] = v.z;
+                x[b][4 * i + 3] = v.w;
             }
-            float x[B][32], xs[B];
+        }
+        uint4 hd[R], qv[R];
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                xs[b] = 0.f;
-                const float4* xp = (const float4*)(X + (int64_t)min(b, nb - 1) * ldx + (int64_t)kb * QK + 32 * s);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float4 v = b < nb ? xp[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    x[b][4 * i] = v.x;
-                    x[b][4 * i + 1] = v.y;
-                    x[b][4 * i + 2] = v.z;
-                    x[b][4 * i + 3] = v.w;
-                }
-#pragma unroll
-                for (int i = 0; i < 32; ++i) xs[b] += x[b][i];
+        for (int r = 0; r < R; ++r) {
+            const int m = min(m0 + r, M - 1);
+            const uint8_t* hp;
+            const uint8_t* qp;
+            if (TILED) {
+                const uint8_t* tb = W + ((size_t)(m >> 4) * nblk + kbc) * (16 * QBLOCK);
+                hp = tb + 16 * (m & 15);
+                qp = tb + ((s & 1) ? 1280 : 256) + 16 * (16 * (s >> 1) + (m & 15));
+            } else {
+                hp = W + ((size_t)m * nblk + kbc) * QBLOCK;
+                qp = hp + 16 + 16 * s;
             }
+            hd[r] = *(const uint4*)hp;
+            qv[r] = *(const uint4*)qp;
+        }
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint4 h = hd[r];
-                const uint32_t sc = s < 4 ? (h.y >> sh) & 63u : ((h.w >> sh) & 15u) | ((h.y >> (sh + 2)) & 0x30u);
-                const uint32_t mn =
-                    s < 4 ? (h.z >> sh) & 63u : ((h.w >> (sh + 4)) & 15u) | ((h.z >> (sh + 2)) & 0x30u);
-                const float dsc = f16_to_f32_hw(h.x & 0xffffu) * (float)sc;
-                const float dmn = f16_to_f32_hw(h.x >> 16) * (float)mn;
-                const uint32_t q[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
-                float lo[B], hi[B];
+        for (int b = 0; b < B; ++b) {
+            xs[b] = 0.f;
 #pragma unroll
-                for (int b = 0; b < B; ++b) lo[b] = hi[b] = 0.f;
+            for (int i = 0; i < 32; ++i) xs[b] += x[b][i];
+        }
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint32_t ql = q[w] & 0x0f0f0f0fu, qh = q[w] & 0xf0f0f0f0u;
+        for (int r = 0; r < R; ++r) {
+            const uint4 h = hd[r];
+            const uint32_t sc = s < 4 ? (h.y >> sh) & 63u : ((h.w >> sh) & 15u) | ((h.y >> (sh + 2)) & 0x30u);
+            const uint32_t mn = s < 4 ? (h.z >> sh) & 63u : ((h.w >> (sh + 4)) & 15u) | ((h.z >> (sh + 2)) & 0x30u);
+            const float dsc = f16_to_f32_hw(h.x & 0xffffu) * (float)sc;
+            const float dmn = f16_to_f32_hw(h.x >> 16) * (float)mn;
+            const uint32_t q[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
+            float lo[B], hi[B];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const float fl = (float)((ql >> (8 * k)) & 0xffu);
-                        const float fh = (float)((qh >> (8 * k)) & 0xffu);
+            for (int b = 0; b < B; ++b) lo[b] = hi[b] = 0.f;
 #pragma unroll
-                        for (int b = 0; b < B; ++b) {
-                            lo[b] = __builtin_fmaf(fl, x[b][4 * w + k], lo[b]);
-                            hi[b] = __builtin_fmaf(fh, x[b][16 + 4 * w + k], hi[b]);
-                        }
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t ql = and_opaque(q[w], 0x0f0f0f0fu), qh = and_opaque(q[w], 0xf0f0f0f0u);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float fl = (float)((ql >> (8 * k)) & 0xffu);
+                    const float fh = (float)((qh >> (8 * k)) & 0xffu);
+#pragma unroll
+                    for (int b = 0; b < B; ++b) {
+                        lo[b] = __builtin_fmaf(fl, x[b][4 * w + k], lo[b]);
+                        hi[b] = __builtin_fmaf(fh, x[b][16 + 4 * w + k], hi[b]);
                     }
                 }
-#pragma unroll
-                for (int b = 0; b < B; ++b) acc[r][b] += dsc * (lo[b] + hi[b] * 0.0625f) - dmn * xs[b];
             }
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[r][b] += dsc * (lo[b] + hi[b] * 0.0625f) - dmn * xs[b];
         }
     }
     // 16-lane rows by DPP; lane 0 of each row keeps the row's sums
@@ -165,8 +178,12 @@ int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64
     const int nblk = K / QK;
     // rows per workgroup: 8 for one or two activation rows, 4 for three or
     // four (keeps the activations, 32 x B floats per thread, and the loads
-    // of all R rows under 256 VGPRs: two waves per SIMD)
-    const int R = B <= 2 ? 8 : 4;
+    // of all R rows under 256 VGPRs: two waves per SIMD); one row of slate's
+    // layout over more than 32 blocks takes 16, since every workgroup reads
+    // all of X (at 4096 x 14336: 13.2 vs 15.6 us per call, 12.1 vs 11.5 at
+    // 14336 x 4096)
+    const bool r16 = B == 1 && nblk > 32 && !tiled;
+    const int R = r16 ? 16 : (B <= 2 ? 8 : 4);
     Q4kTargets tg{};
     int grp = 0;
     for (int i = 0; i < n; ++i) {
@@ -180,7 +197,10 @@ int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64
     tg.n = n;
     tg.grp_end = grp;
     const int nw = std::min(GEMV_WAVES, (nblk + 7) / 8);
-    if (B == 1) launch_gemv<1, 8>(tg, tiled, X, ldx, B, Y, ldy, nblk, nw, s, ev_start, ev_stop);
+    if (r16)
+        SH_LAUNCH(ev_start, ev_stop, (q4k_gemv_kernel<1, 16, false>), dim3(tg.grp_end), dim3(64 * nw), 0, s, tg, X,
+                  ldx, B, Y, ldy, nblk);
+    else if (B == 1) launch_gemv<1, 8>(tg, tiled, X, ldx, B, Y, ldy, nblk, nw, s, ev_start, ev_stop);
     else if (B == 2) launch_gemv<2, 8>(tg, tiled, X, ldx, B, Y, ldy, nblk, nw, s, ev_start, ev_stop);
     else launch_gemv<4, 4>(tg, tiled, X, ldx, B, Y, ldy, nblk, nw, s, ev_start, ev_stop);
     SH_CHECK_LAUNCH();

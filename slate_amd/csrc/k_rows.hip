@@ -614,7 +614,8 @@ int launch_pack_batch(const int32_t* slot, const int32_t* pos0, const int32_t* n
 
 // ---------------------------------------------------------------------------
 // f32 weights.  Y[b, m] = sum_k X[b, k] * W[m, k]: one wave per output row m,
-// lanes stride K, wave reduction; every batch row reuses the loaded W row.
+// lanes stride K, wave reduction; up to 16 batch rows per pass reuse each
+// loaded W element (one pass over W for B <= 16).
 template <int BT>
 __global__ __launch_bounds__(256) void mm_f32_kernel(float* __restrict__ Y, const float* __restrict__ X,
                                                      const float* __restrict__ W, int B, int M, int K,
@@ -624,46 +625,72 @@ __global__ __launch_bounds__(256) void mm_f32_kernel(float* __restrict__ Y, cons
     if (m >= M) return;
     const float* w = W + (size_t)m * K;
     for (int b0 = 0; b0 < B; b0 += BT) {
+        const int nb = min(BT, B - b0);
         float acc[BT];
 #pragma unroll
         for (int i = 0; i < BT; ++i) acc[i] = 0.f;
         for (int k = lane; k < K; k += 64) {
-            float wv = w[k];
+            const float wv = w[k];
 #pragma unroll
             for (int i = 0; i < BT; ++i)
-                if (b0 + i < B) acc[i] = __builtin_fmaf(wv, X[(size_t)(b0 + i) * K + k], acc[i]);
+                if (i < nb) acc[i] = __builtin_fmaf(wv, X[(size_t)(b0 + i) * K + k], acc[i]);
         }
 #pragma unroll
         for (int i = 0; i < BT; ++i) {
             float v = acc[i];
             for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            if (lane == 0 && b0 + i < B) Y[(size_t)(b0 + i) * ldy + m] = v;
+            if (lane == 0 && i < nb) Y[(size_t)(b0 + i) * ldy + m] = v;
         }
     }
 }
 
 int launch_mm_f32(float* Y, const float* X, const float* W, int B, int M, int K, int ldy, hipStream_t s) {
     if (B <= 0 || M <= 0) return 0;
-    hipLaunchKernelGGL(mm_f32_kernel<8>, dim3((M + 3) / 4), dim3(256), 0, s, Y, X, W, B, M, K, ldy);
+    if (B <= 4)
+        hipLaunchKernelGGL(mm_f32_kernel<4>, dim3((M + 3) / 4), dim3(256), 0, s, Y, X, W, B, M, K, ldy);
+    else
+        hipLaunchKernelGGL(mm_f32_kernel<16>, dim3((M + 3) / 4), dim3(256), 0, s, Y, X, W, B, M, K, ldy);
     SH_CHECK_LAUNCH();
     return 0;
 }
 
 // C[b, n] = sum_k X[b, k] * W[k, n] (W is [K, N] for linear_batch, backend.h:58-61).
-__global__ void linear_batch_kernel(float* __restrict__ C, const float* __restrict__ X,
-                                    const float* __restrict__ W, int B, int K, int N) {
-    int n = blockIdx.x * blockDim.x + threadIdx.x;
-    int b = blockIdx.y;
-    if (n >= N) return;
-    const float* x = X + (size_t)b * K;
-    float acc = 0.f;
-    for (int k = 0; k < K; ++k) acc = __builtin_fmaf(x[k], W[(size_t)k * N + n], acc);
-    C[(size_t)b * N + n] = acc;
+// A workgroup owns 64 columns and LB_ROWS batch rows: lanes over n
+// (coalesced W rows), the four waves over k (k = wave mod 4), each W element
+// loaded once for all the rows, the waves' sums combined in LDS in a fixed
+// order.
+constexpr int LB_ROWS = 8;
+__global__ __launch_bounds__(256) void linear_batch_kernel(float* __restrict__ C, const float* __restrict__ X,
+                                                           const float* __restrict__ W, int B, int K, int N) {
+    __shared__ float red[4][LB_ROWS][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int n = blockIdx.x * 64 + lane;
+    const int b0 = blockIdx.y * LB_ROWS;
+    const int nb = min(LB_ROWS, B - b0);
+    float acc[LB_ROWS];
+#pragma unroll
+    for (int i = 0; i < LB_ROWS; ++i) acc[i] = 0.f;
+    if (n < N) {
+        for (int k = wv; k < K; k += 4) {
+            const float w = W[(size_t)k * N + n];
+#pragma unroll
+            for (int i = 0; i < LB_ROWS; ++i)
+                if (i < nb) acc[i] = __builtin_fmaf(X[(size_t)(b0 + i) * K + k], w, acc[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < LB_ROWS; ++i) red[wv][i][lane] = acc[i];
+    __syncthreads();
+    if (wv == 0 && n < N) {
+        for (int i = 0; i < nb; ++i)
+            C[(size_t)(b0 + i) * N + n] = (red[0][i][lane] + red[1][i][lane]) + (red[2][i][lane] + red[3][i][lane]);
+    }
 }
 
 int launch_linear_batch(float* C, const float* X, const float* W, int B, int K, int N, hipStream_t s) {
     if (B <= 0 || N <= 0) return 0;
-    hipLaunchKernelGGL(linear_batch_kernel, dim3((N + 255) / 256, B), dim3(256), 0, s, C, X, W, B, K, N);
+    hipLaunchKernelGGL(linear_batch_kernel, dim3((N + 63) / 64, (B + LB_ROWS - 1) / LB_ROWS), dim3(256), 0, s, C,
+                       X, W, B, K, N);
     SH_CHECK_LAUNCH();
     return 0;
 }

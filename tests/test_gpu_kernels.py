@@ -317,6 +317,43 @@ def test_matvec_linear_batch_random(hip, orc):
         assert np.max(np.abs(host(Cd, np.float32, (Bn, N)) - want)) < 1e-4
 
 
+@pytest.mark.parametrize("Bn,K,N", [(1, 64, 300), (13, 300, 70), (37, 1000, 129)])
+def test_linear_batch_row_blocks(hip, orc, Bn, K, N):
+    """linear_batch (backend.h:58-61) with batch counts off the kernel's
+    8-row blocks and column counts off its 64-column groups."""
+    rng = np.random.default_rng(Bn * 1000 + N)
+    X = rng.normal(0, 1, (Bn, K)).astype(np.float32)
+    W = rng.normal(0, 0.5, (K, N)).astype(np.float32)
+    Cd = DB(Bn * N * 4)
+    hip.linear_batch(Cd.p, dev(X).p, dev(W).p, Bn, K, N)
+    want = np.empty((Bn, N), np.float32)
+    orc.lib.orc_linear_batch(fp(want), fp(X), fp(W), Bn, K, N)
+    assert np.max(np.abs(host(Cd, np.float32, (Bn, N)) - want)) < 1e-4
+    check(0, "linear_batch")
+
+
+@pytest.mark.parametrize("L,D", [(1, 16), (7, 80), (1000, 128), (3000, 64), (300, 200), (40, 1100)])
+def test_attention_step_long_contexts(hip, L, D):
+    """The vtable's single-head attention (backend_cpu.c:117-166) at long
+    contexts and head sizes off the wave width, against float64 softmax
+    attention: out within 1e-5 absolute (test_backend.c's bound), and the
+    scratch holds the normalised probabilities, as the reference leaves it."""
+    rng = np.random.default_rng(L + D)
+    q = rng.normal(0, 1, D).astype(np.float32)
+    K = rng.normal(0, 1, (L, D)).astype(np.float32)
+    V = rng.normal(0, 1, (L, D)).astype(np.float32)
+    o = DB(D * 4)
+    sc = DB(L * 4)
+    hip.attention_step(o.p, dev(q).p, dev(K).p, dev(V).p, sc.p, L, D)
+    hip.sync()
+    check(0, "attention_step")
+    s = (K.astype(np.float64) @ q.astype(np.float64)) / np.sqrt(D)
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    assert np.max(np.abs(host(sc, np.float32, L) - p)) < 1e-6
+    assert np.max(np.abs(host(o, np.float32, D) - p @ V.astype(np.float64))) < 1e-5
+
+
 # ------------------------------------------------------------ RoPE
 def test_rope_rows_bitexact_golden(hip, golden):
     x, y, pos = golden["rope_x"], golden["rope_y"], golden["rope_pos"]
