@@ -55,6 +55,7 @@ bool device_ok();            // a gfx950 device was opened
 struct Knobs {
     int attn_wave = 1;     // SLATE_HIP_ATTN_WAVE=0: phased decode attention for every shape
     int attn_rope = 1;     // SLATE_HIP_ATTN_ROPE: 0 RoPE/append in their own kernel, 2 fused into the phased kernel
+    int attn_xcd = 1;      // SLATE_HIP_ATTN_XCD=0: decode attention partials merged by their own kernel
     int attn_mfma = 1;     // SLATE_HIP_ATTN_MFMA: prompt blocks on the MFMA kernel 0 never, 1 when the
                            // step's prompt work outweighs its decode work, 2 whenever a step has prompt chunks
     int q4k_w = 8;         // SLATE_HIP_Q4K_W: waves per decode workgroup (4 or 8)

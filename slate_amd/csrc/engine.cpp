@@ -82,6 +82,7 @@ struct slate_hip_llama {
     bool prompt_mfma = false;      // prompt-chunk blocks may go to the MFMA prompt attention kernel
     bool step_prompt_mfma = false; // ... and do in the step being enqueued
     float *att_po = nullptr, *att_pml = nullptr;
+    int32_t* att_xcd = nullptr;     // per-XCD decode attention queues (attention_xcd_view)
     Act16 act{};
     Act8 act8{};                   // allocated with the first Q8_0 linear
     int32_t *d_desc = nullptr, *d_tok = nullptr, *tok_off = nullptr, *tok2seq = nullptr, *tok_pos = nullptr,
@@ -198,6 +199,10 @@ int alloc_runtime(slate_hip_llama* m) {
     if (dalloc(m, &m->att_po, np)) return -2;
     m->att_pml = m->att_po + (size_t)T * c.n_heads * ((c.max_seq + attn_chunk_size() - 1) / attn_chunk_size()) *
                                  c.head_dim;
+    // decode steps (one token per sequence, at most max_slots rows) merge
+    // the attention chunks inside the attention kernel from per-XCD queues
+    if (dalloc(m, &m->att_xcd, attention_xcd_ints(m->max_slots, c.n_kv_heads, c.max_seq))) return -2;
+    attention_xcd_probe();
     // Q4_K activation operand for the widest matmul input (max(D, H)), T_pad rows
     const int Kmax = std::max(D, H);
     char* fr = nullptr;
@@ -527,8 +532,12 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if (rc) return rc;
     if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
     // the decode attention work units depend only on positions: once per step
+    AttnXcd xq{};
+    const bool xcd = m->step_one_each && T <= m->max_slots &&
+                     attention_xcd_merge(T, c.n_heads, c.n_kv_heads, hd, c.max_seq, true);
+    if (xcd) xq = attention_xcd_view(m->att_xcd, m->max_slots, c.n_kv_heads, c.max_seq);
     if ((rc = launch_attention_pairs(d_blk, m->n_dec, m->tok_pos, m->tok2seq, m->kv_base, T, c.n_heads, c.max_seq,
-                                      m->att_pml, s))) return rc;
+                                      m->att_pml, s, xcd ? &xq : nullptr, c.n_kv_heads))) return rc;
     const int tpad = row_pad(T);
     int S_prev = 0;
     RowNorm rn{};
@@ -569,7 +578,7 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
                 rc = launch_attention_rope(m->att, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
                                            m->rope_cs, rn, m->tok_pos, T, c.n_heads, c.n_kv_heads, hd,
                                            m->head_stride, c.max_seq, m->att_po, m->att_pml, gi.q4 ? &a : nullptr, s,
-                                           prof_ev(m, ea), prof_ev(m, eb), m->kv_f16);
+                                           prof_ev(m, ea), prof_ev(m, eb), m->kv_f16, xcd ? &xq : nullptr);
             if (rc < 0) return rc;
             if (rc > 0) {
                 if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,

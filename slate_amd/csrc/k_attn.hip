@@ -11,10 +11,14 @@
 // causal limit applied per token.  Each unit leaves a partial (running max,
 // running sum, unnormalised output) per (token, q head, chunk); a merge kernel
 // combines the chunks with log-sum-exp rescaling.
+#include <algorithm>
+#include <atomic>
+
 #include "launch.h"
 #include "act16.h"
 #include "lanes.h"
 #include "rowops.h"
+#include "mfma.h"
 
 namespace slate_hip {
 
@@ -495,20 +499,16 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_phased_rope_kernel(
 // attn_block_kernel writes it.
 // With ROPE the unit first runs attn_rope_prologue (q from LDS afterwards).
 template <int HD, int G, typename KVT, bool ROPE>
-__device__ __forceinline__ void attn_dec_wave_body(
-    const float* q, const KVT* Kp, const KVT* Vp, const int32_t* pairs, int Hq, int64_t head_stride, int nch_max,
-    float* po, float* pml, const AttnRope& fr, int Hkv) {
+__device__ __forceinline__ void attn_dec_wave_unit(
+    const float* q, const KVT* Kp, const KVT* Vp, const AttnUnit& un, int h, int Hq, int64_t head_stride,
+    int nch_max, float* po, float* pml, const AttnRope& fr, int Hkv) {
     constexpr int NV = HD / 32;                    // float4 per lane per row
     constexpr int KW = ATT_CHUNK / 4;              // keys per wave
     constexpr int IT = KW / 8;                     // rounds of 8 keys
     __shared__ float4 s_o[4][4][G][HD / 4];        // [wave][16-lane row][head][dims]
     __shared__ float s_m[4][G], s_l[4][G];
     __shared__ float s_q[ROPE ? G : 1][ROPE ? HD : 1];
-    // work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
-    // wrote; the units past its count are the grid's empty tail
-    const AttnUnit un = attn_unit(pairs, blockIdx.x);
-    if ((int)blockIdx.x >= un.n) return;
-    const int c = un.c, h = blockIdx.z, t = un.t, p = un.p;
+    const int c = un.c, t = un.t, p = un.p;
     const int k0 = c * ATT_CHUNK;
     if (k0 > p) return;                            // merge never reads chunks past a token's end
     const int nk = min(p + 1 - k0, ATT_CHUNK);
@@ -674,6 +674,18 @@ __device__ __forceinline__ void attn_dec_wave_body(
     }
 }
 
+// Work unit blockIdx.x of the (token, chunk) list that attn_pairs_kernel
+// wrote (kv head blockIdx.z); the units past its count are the grid's
+// empty tail.
+template <int HD, int G, typename KVT, bool ROPE>
+__device__ __forceinline__ void attn_dec_wave_body(
+    const float* q, const KVT* Kp, const KVT* Vp, const int32_t* pairs, int Hq, int64_t head_stride, int nch_max,
+    float* po, float* pml, const AttnRope& fr, int Hkv) {
+    const AttnUnit un = attn_unit(pairs, blockIdx.x);
+    if ((int)blockIdx.x >= un.n) return;
+    attn_dec_wave_unit<HD, G, KVT, ROPE>(q, Kp, Vp, un, blockIdx.z, Hq, head_stride, nch_max, po, pml, fr, Hkv);
+}
+
 template <int HD, int G, typename KVT>
 __global__ __launch_bounds__(ATT_THREADS) void attn_dec_wave_kernel(
     const float* __restrict__ q, const KVT* __restrict__ Kp, const KVT* __restrict__ Vp,
@@ -693,10 +705,89 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_kernel(
     attn_dec_wave_body<HD, G, KVT, true>(nullptr, Kp, Vp, pairs, Hq, head_stride, nch_max, po, pml, fr, Hkv);
 }
 
-// out[t, hq, :] = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c.  One wave per
-// 256 output elements of a token row (lane: 4 consecutive elements of one
-// head); with `act` the row also goes out as the Q4_K activation operand
-// (padding rows t >= T as zeros).
+// Chunk partials of the merge: plain loads (the merge kernel runs after the
+// launch that wrote them), or loads that miss in L1 and read L2 (the merge
+// inside the decode kernel reads lines other units of the same launch wrote
+// to L2 from other CUs of its XCD; buffer loads with sc0, offsets in bytes
+// from po and pml, outside them zero).
+struct PartPlain {
+    const float* po;
+    const float* pml;
+    __device__ __forceinline__ float2 ml(size_t pc) const { return *(const float2*)(pml + pc * 2); }
+    __device__ __forceinline__ float4 o(size_t pc, int HD, int d) const {
+        return *(const float4*)(po + pc * HD + d);
+    }
+};
+struct PartL2 {
+    __amdgpu_buffer_rsrc_t po, pml;
+    __device__ __forceinline__ float2 ml(size_t pc) const {
+        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(pml, (int)(pc * 8), 0, 1));
+    }
+    __device__ __forceinline__ float4 o(size_t pc, int HD, int d) const {
+        return __builtin_bit_cast(float4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(po, (int)((pc * HD + d) * 4), 0, 1));
+    }
+};
+
+// out = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c over the nch chunks of
+// (token, q head) p0 / nch_max, for dims d .. d+3.  The first MB chunks'
+// (max, sum) and outputs are loaded in one batch (clamped to the last
+// chunk, used under a predicate): one round trip for contexts up to MB
+// chunks; the max over every chunk is taken before any chunk is
+// accumulated, in chunk order.
+template <class P, int MB = 8>
+__device__ __forceinline__ float4 merge_chunks(const P& pp, size_t p0, int nch, int HD, int d) {
+    float2 ml[MB];
+    float4 ov[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const size_t pc = p0 + min(i, max(nch - 1, 0));
+        ml[i] = pp.ml(pc);
+        ov[i] = pp.o(pc, HD, d);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+        if (i < nch) M = fmaxf(M, ml[i].x);
+    for (int c0 = MB; c0 < nch; c0 += MB) {
+        float mv[MB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) mv[i] = pp.ml(p0 + min(c0 + i, nch - 1)).x;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            if (c0 + i < nch) M = fmaxf(M, mv[i]);
+    }
+    float den = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+        if (i < nch) {
+            const float f = expf(ml[i].x - M);
+            den += f * ml[i].y;
+            acc.x += f * ov[i].x; acc.y += f * ov[i].y; acc.z += f * ov[i].z; acc.w += f * ov[i].w;
+        }
+    for (int c0 = MB; c0 < nch; c0 += MB) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const size_t pc = p0 + min(c0 + i, nch - 1);
+            ml[i] = pp.ml(pc);
+            ov[i] = pp.o(pc, HD, d);
+        }
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            if (c0 + i < nch) {
+                const float f = expf(ml[i].x - M);
+                den += f * ml[i].y;
+                acc.x += f * ov[i].x; acc.y += f * ov[i].y; acc.z += f * ov[i].z; acc.w += f * ov[i].w;
+            }
+    }
+    const float inv = 1.0f / den;
+    return make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+}
+
+// One wave per 256 output elements of a token row (lane: 4 consecutive
+// elements of one head); with `act` the row also goes out as the Q4_K
+// activation operand (padding rows t >= T as zeros).
 __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ po,
                                                          const float* __restrict__ pml,
                                                          const int32_t* __restrict__ tok_pos, int T, int Hq,
@@ -712,61 +803,181 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
         const int hq = e / HD, d = e - hq * HD;
         const int L = tok_pos[t] + 1;
         const int nch = min((L + ATT_CHUNK - 1) / ATT_CHUNK, nch_max);
-        const size_t p0 = ((size_t)t * Hq + hq) * nch_max;
-        // the first eight chunks' (max, sum) and outputs are loaded in one
-        // batch (clamped to the last chunk, used under a predicate): one
-        // round trip for contexts up to eight chunks; the max over every
-        // chunk is taken before any chunk is accumulated, in chunk order
-        constexpr int MB = 8;
-        float2 ml[MB];
-        float4 ov[MB];
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-            const size_t pc = p0 + min(i, max(nch - 1, 0));
-            ml[i] = *(const float2*)(pml + pc * 2);
-            ov[i] = *(const float4*)(po + pc * HD + d);
-        }
-        float M = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-            if (i < nch) M = fmaxf(M, ml[i].x);
-        for (int c0 = MB; c0 < nch; c0 += MB) {
-            float mv[MB];
-#pragma unroll
-            for (int i = 0; i < MB; ++i) mv[i] = pml[(p0 + min(c0 + i, nch - 1)) * 2];
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-                if (c0 + i < nch) M = fmaxf(M, mv[i]);
-        }
-        float den = 0.f;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-            if (i < nch) {
-                const float f = expf(ml[i].x - M);
-                den += f * ml[i].y;
-                acc.x += f * ov[i].x; acc.y += f * ov[i].y; acc.z += f * ov[i].z; acc.w += f * ov[i].w;
-            }
-        for (int c0 = MB; c0 < nch; c0 += MB) {
-#pragma unroll
-            for (int i = 0; i < MB; ++i) {
-                const size_t pc = p0 + min(c0 + i, nch - 1);
-                ml[i] = *(const float2*)(pml + pc * 2);
-                ov[i] = *(const float4*)(po + pc * HD + d);
-            }
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-                if (c0 + i < nch) {
-                    const float f = expf(ml[i].x - M);
-                    den += f * ml[i].y;
-                    acc.x += f * ov[i].x; acc.y += f * ov[i].y; acc.z += f * ov[i].z; acc.w += f * ov[i].w;
-                }
-        }
-        const float inv = 1.0f / den;
-        res = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        res = merge_chunks(PartPlain{po, pml}, ((size_t)t * Hq + hq) * nch_max, nch, HD, d);
         *(float4*)(out + (size_t)t * D + e) = res;
     }
     if (act) act16_store_block(a, t, kb, lane, res);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention with the chunk merge inside (steps in which every
+// sequence adds one token).  Workgroups are dealt to the eight XCDs in turn
+// (workgroup i to XCD i % 8) and each XCD has its own L2; the workgroups of
+// XCD x take their units from queue x, which holds every chunk of the
+// (token, kv head) pairs assigned to it.  The unit that
+// finishes a pair's last chunk (an atomic count per pair) merges the pair's
+// G heads: its partials were written by units of the same XCD, whose stores
+// completed in that L2 before they counted (a wait for the stores, a
+// barrier, then the count), and it reads them with loads that miss in L1.
+// No writeback of L2 to memory is needed, as it would be across XCDs.
+
+__global__ void xcc_probe_kernel(int32_t* out) {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    if (threadIdx.x == 0) out[blockIdx.x] = (int32_t)x;
+}
+
+static int device_cus();
+
+// Whether workgroup i of a launch runs on XCD i % 8 of an eight-XCD device
+// (read from the hardware register by 64 workgroups), once per process.
+static std::atomic<int> g_xcd_rr{-1};
+bool attention_xcd_probe() {
+    int v = g_xcd_rr.load();
+    if (v >= 0) return v == 1;
+    bool ok = device_cus() == 256;
+    int32_t* d = nullptr;
+    int32_t h[64];
+    if (ok) ok = hipMalloc(&d, sizeof h) == hipSuccess;
+    if (ok) {
+        hipLaunchKernelGGL(xcc_probe_kernel, dim3(64), dim3(64), 0, nullptr, d);
+        ok = hipGetLastError() == hipSuccess && hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess;
+        (void)hipFree(d);
+    }
+    for (int i = 0; ok && i < 64; ++i) ok = (h[i] & 15) == i % 8;
+    g_xcd_rr.store(ok ? 1 : 0);
+    return ok;
+}
+
+size_t attention_xcd_ints(int max_tok, int Hkv, int max_pos) {
+    const size_t nch = (size_t)(max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
+    const size_t cap = ((size_t)max_tok * Hkv + 7) / 8 * nch;
+    const size_t fixed = (8 + (size_t)max_tok * Hkv + 3) / 4 * 4;
+    return fixed + 8 * cap * 4;
+}
+
+// Layout of attention_xcd_ints(max_tok, Hkv, max_pos) int32s from a
+// 16-byte aligned base: len, arrive, then the eight queues.
+AttnXcd attention_xcd_view(int32_t* base, int max_tok, int Hkv, int max_pos) {
+    const size_t fixed = (8 + (size_t)max_tok * Hkv + 3) / 4 * 4;
+    AttnXcd x{};
+    x.len = base;
+    x.arrive = x.len + 8;
+    x.units = (int4*)(base + fixed);
+    x.max_tok = max_tok;
+    x.cap = (int)(((size_t)max_tok * Hkv + 7) / 8 * ((max_pos + ATT_CHUNK - 1) / ATT_CHUNK));
+    return x;
+}
+
+// The per-XCD queues of the step's decode tokens, one workgroup: per round
+// of 1024 tokens, eight block-wide scans of the tokens' unit counts per
+// queue; every pair's arrival count reset.
+__global__ __launch_bounds__(1024) void attn_xcd_queues_kernel(const int32_t* __restrict__ dec_t0, int n_dec,
+                                                               const int32_t* __restrict__ tok_pos,
+                                                               const int32_t* __restrict__ tok2seq,
+                                                               const int64_t* __restrict__ kv_base, int nch_max,
+                                                               int Hkv, AttnXcd xq) {
+    __shared__ int s_scan[8][1024];
+    __shared__ int s_base[8];
+    const int tid = threadIdx.x;
+    if (tid < 8) s_base[tid] = 0;
+    __syncthreads();
+    for (int i0 = 0; i0 < n_dec; i0 += 1024) {
+        const int i = i0 + tid;
+        int n = 0, t = 0, p = 0;
+        int64_t kvb = 0;
+        if (i < n_dec) {
+            t = dec_t0 ? dec_t0[i] : i;
+            p = tok_pos[t];
+            kvb = kv_base[tok2seq[t]];
+            n = min((p + ATT_CHUNK) / ATT_CHUNK, nch_max);
+        }
+        int cnt[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) cnt[x] = 0;
+        for (int h = 0; h < Hkv && i < n_dec; ++h) {
+            const int x = (t * Hkv + h) & 7;
+#pragma unroll
+            for (int y = 0; y < 8; ++y) cnt[y] += y == x ? n : 0;
+            xq.arrive[t * Hkv + h] = 0;
+        }
+#pragma unroll
+        for (int x = 0; x < 8; ++x) s_scan[x][tid] = cnt[x];
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            int v[8];
+#pragma unroll
+            for (int x = 0; x < 8; ++x) v[x] = tid >= o ? s_scan[x][tid - o] : 0;
+            __syncthreads();
+#pragma unroll
+            for (int x = 0; x < 8; ++x) s_scan[x][tid] += v[x];
+            __syncthreads();
+        }
+        int run[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) run[x] = s_base[x] + s_scan[x][tid] - cnt[x];
+        for (int h = 0; h < Hkv && i < n_dec; ++h) {
+            const int x = (t * Hkv + h) & 7;
+            int r = 0;
+#pragma unroll
+            for (int y = 0; y < 8; ++y) r = y == x ? run[y] : r;
+            int4* q = xq.units + (size_t)x * xq.cap + r;
+            for (int c = 0; c < n; ++c)
+                q[c] = make_int4(t * 65536 + c, p, (int)(uint32_t)((uint64_t)kvb & 0xffffffffu),
+                                 (int)((uint32_t)((uint64_t)kvb >> 32) | ((uint32_t)h << 24)));
+#pragma unroll
+            for (int y = 0; y < 8; ++y) run[y] += y == x ? n : 0;
+        }
+        __syncthreads();
+        if (tid == 1023)
+#pragma unroll
+            for (int x = 0; x < 8; ++x) s_base[x] += s_scan[x][1023];
+        __syncthreads();
+    }
+    if (tid < 8) xq.len[tid] = s_base[tid];
+}
+
+// One unit per workgroup: workgroup i runs on XCD i % 8 (the dispatch order,
+// checked once per process by attention_xcd_probe) and takes unit i / 8 of
+// that XCD's queue; the grid covers the longest queue and the surplus
+// workgroups exit.
+template <int HD, int G, typename KVT>
+__global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_xcd_kernel(
+    const KVT* Kp, const KVT* Vp, int Hq, int Hkv, int64_t head_stride, int nch_max, float* __restrict__ po,
+    float* __restrict__ pml, uint32_t po_bytes, uint32_t pml_bytes, AttnRope fr, AttnXcd xq,
+    float* __restrict__ out, Act16 a, int act) {
+    constexpr int NB = G * HD / 256;                   // operand blocks of a kv head's G heads
+    __shared__ int s_last;
+    const int xcc = blockIdx.x & 7, u = blockIdx.x >> 3;
+    if (u >= xq.len[xcc]) return;                      // workgroup-uniform
+    const int4 d = xq.units[(size_t)xcc * xq.cap + u];
+    AttnUnit un;
+    un.n = 0;
+    un.t = d.x >> 16;
+    un.c = d.x & 0xffff;
+    un.p = d.y;
+    un.kvb = (int64_t)(((uint64_t)((uint32_t)d.w & 0xffffffu) << 32) | (uint64_t)(uint32_t)d.z);
+    const int h = (int)((uint32_t)d.w >> 24);
+    attn_dec_wave_unit<HD, G, KVT, true>(nullptr, Kp, Vp, un, h, Hq, head_stride, nch_max, po, pml, fr, Hkv);
+    SH_WAIT_VMCNT(0);                                  // this thread's partial stores are in L2
+    __syncthreads();
+    const int nch = min((un.p + ATT_CHUNK) / ATT_CHUNK, nch_max);
+    if (threadIdx.x == 0) {
+        s_last = atomicAdd(&xq.arrive[un.t * Hkv + h], 1) == nch - 1;
+        if (s_last) atomicExch(&xq.arrive[un.t * Hkv + h], 0);   // every chunk has counted: ready for the next layer
+    }
+    __syncthreads();
+    if (!s_last) return;
+    const PartL2 pp{__builtin_amdgcn_make_buffer_rsrc(po, 0, (int)po_bytes, 0x00020000),
+                    __builtin_amdgcn_make_buffer_rsrc(pml, 0, (int)pml_bytes, 0x00020000)};
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    for (int w = wv; w < NB; w += ATT_THREADS / 64) {
+        const int e = h * G * HD + w * 256 + 4 * lane;
+        const int hq = e / HD, dd = e - hq * HD;
+        const float4 res = merge_chunks(pp, ((size_t)un.t * Hq + hq) * nch_max, nch, HD, dd);
+        *(float4*)(out + (size_t)un.t * Hq * HD + e) = res;
+        if (act) act16_store_block(a, un.t, h * NB + w, lane, res);
+    }
 }
 
 struct AttnArgs {
@@ -980,11 +1191,89 @@ static int launch_rope_hd(int G, bool f16, dim3 grid, hipStream_t s, hipEvent_t 
     }
 }
 
+// Compute units of the device (for persistent grids).
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+bool attention_xcd_merge(int T, int Hq, int Hkv, int HD, int max_pos, bool has_act) {
+    (void)has_act;
+    // workgroup i on XCD i % 8, as probed (attention_xcd_probe) for this device
+    if (!knobs().attn_xcd || rope_fused() != 1 || !wave_kernel() || T <= 0 || T > ATT_WAVE_MAX_TOKENS ||
+        Hkv <= 0 || Hq % Hkv != 0 || g_xcd_rr.load() != 1)
+        return false;
+    const int G = Hq / Hkv;
+    if (!(HD == 32 || HD == 64 || HD == 128) || G * HD > 512 || (G * HD) % 256 != 0) return false;
+    const double nch = (double)((max_pos + ATT_CHUNK - 1) / ATT_CHUNK);
+    return (double)T * Hq * nch * HD * 4.0 < 2147483648.0;   // buffer offsets of the partials
+}
+
+template <int HD, int G, typename KVT>
+static void launch_xcd_t(hipStream_t s, hipEvent_t ev0, hipEvent_t ev1, const void* Kp, const void* Vp, int Hq,
+                         int Hkv, int64_t head_stride, int nch_max, float* po, float* pml, uint32_t po_bytes,
+                         uint32_t pml_bytes, const AttnRope& fr, const AttnXcd& xq, float* out, const Act16* act) {
+    if constexpr (G * HD <= 512 && (G * HD) % 256 == 0) {
+        // a queue holds at most ceil(T * Hkv / 8) pairs of at most nch_max units
+        const int grid = 8 * ((xq.max_tok_step * Hkv + 7) / 8) * nch_max;
+        SH_LAUNCH(ev0, ev1, (attn_dec_rope_xcd_kernel<HD, G, KVT>), dim3(grid), dim3(ATT_THREADS), 0, s,
+                  (const KVT*)Kp, (const KVT*)Vp, Hq, Hkv, head_stride, nch_max, po, pml, po_bytes, pml_bytes, fr,
+                  xq, out, act ? *act : Act16{}, act ? 1 : 0);
+    }
+}
+
+template <int HD, int G>
+static void launch_xcd_g(bool f16, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1, const void* Kp, const void* Vp,
+                         int Hq, int Hkv, int64_t head_stride, int nch_max, float* po, float* pml, uint32_t po_bytes,
+                         uint32_t pml_bytes, const AttnRope& fr, const AttnXcd& xq, float* out, const Act16* act) {
+    if (f16)
+        launch_xcd_t<HD, G, _Float16>(s, ev0, ev1, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml, po_bytes,
+                                      pml_bytes, fr, xq, out, act);
+    else
+        launch_xcd_t<HD, G, float>(s, ev0, ev1, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml, po_bytes, pml_bytes,
+                                   fr, xq, out, act);
+}
+
 int launch_attention_rope(float* out, void* Kp, void* Vp, const float* part, int nsplit, int64_t split_stride,
                           int qkv_ld, const float* cs, const RowNorm& rn, const int32_t* tok_pos, int T, int Hq,
                           int Hkv, int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool kv_f16) {
+                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool kv_f16, const AttnXcd* xq) {
     if (T <= 0) return 0;
+    if (xq && T <= xq->max_tok && (!act || ((Hq * HD) % 256 == 0 && act->K == Hq * HD)) &&
+        attention_xcd_merge(T, Hq, Hkv, HD, max_pos, act != nullptr)) {
+        const int G = Hq / Hkv;
+        const int nch_max = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
+        const AttnRope fr{part, nsplit, split_stride, qkv_ld, cs, rn, Kp, Vp};
+        const uint32_t po_bytes = (uint32_t)((size_t)T * Hq * nch_max * HD * 4);
+        const uint32_t pml_bytes = (uint32_t)((size_t)T * Hq * nch_max * 2 * 4);
+        AttnXcd x = *xq;
+        x.max_tok_step = T;
+        if (HD == 128 && G == 2)
+            launch_xcd_g<128, 2>(kv_f16, s, ev_start, ev_stop, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml,
+                                 po_bytes, pml_bytes, fr, x, out, act);
+        else if (HD == 128 && G == 4)
+            launch_xcd_g<128, 4>(kv_f16, s, ev_start, ev_stop, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml,
+                                 po_bytes, pml_bytes, fr, x, out, act);
+        else if (HD == 64 && G == 4)
+            launch_xcd_g<64, 4>(kv_f16, s, ev_start, ev_stop, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml,
+                                po_bytes, pml_bytes, fr, x, out, act);
+        else if (HD == 64 && G == 8)
+            launch_xcd_g<64, 8>(kv_f16, s, ev_start, ev_stop, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml,
+                                po_bytes, pml_bytes, fr, x, out, act);
+        else if (HD == 32 && G == 8)
+            launch_xcd_g<32, 8>(kv_f16, s, ev_start, ev_stop, Kp, Vp, Hq, Hkv, head_stride, nch_max, po, pml,
+                                po_bytes, pml_bytes, fr, x, out, act);
+        else
+            return 1;
+        SH_CHECK_LAUNCH();
+        return 0;
+    }
     if (rope_fused() == 0 || Hkv <= 0 || Hq % Hkv != 0 ||
         !(HD == 32 || HD == 64 || HD == 128))
         return 1;
@@ -1022,7 +1311,8 @@ int launch_attention_ragged(float* out, const float* q, const float* Kp, const f
 }
 
 int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, const int32_t* tok2seq,
-                           const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s) {
+                           const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s,
+                           const AttnXcd* xq, int Hkv) {
     const int nch_max = (max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
     if (n_dec <= 0) return 0;
     if (n_dec >= 32768 || nch_max > 65536) {
@@ -1032,6 +1322,16 @@ int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_
     hipLaunchKernelGGL(attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, tok2seq, kv_base,
                        nch_max, attn_unit_list(pml, T, Hq, nch_max));
     SH_CHECK_LAUNCH();
+    if (xq) {
+        // every decode token's pairs must fit the queues and the arrival counts
+        if (Hkv <= 0 || Hkv > 127 || T > xq->max_tok) {
+            set_error(-1, "attention: %d tokens x %d kv heads exceed the per-XCD queues", T, Hkv);
+            return -1;
+        }
+        hipLaunchKernelGGL(attn_xcd_queues_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, tok2seq,
+                           kv_base, nch_max, Hkv, *xq);
+        SH_CHECK_LAUNCH();
+    }
     return 0;
 }
 

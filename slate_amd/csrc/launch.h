@@ -67,12 +67,36 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
 // (what launch_rope_kv does) and the attention of launch_attention_blocks in
 // one kernel plus the merge.  Returns 1, launching nothing, when the shape
 // is not one the fused kernel covers (the caller then runs the two paths).
+// Decode attention work queues, one per XCD (attention_xcd_* below): the
+// chunk units of (token t, kv head h) all go to queue (t * Hkv + h) % 8, so
+// the unit that finishes a pair's last chunk can merge the pair's partials
+// from its own XCD's L2 inside the attention kernel.
+struct AttnXcd {
+    int32_t* len;       // [8] units per queue
+    int32_t* arrive;    // [max_tok * Hkv] finished chunks per (token, kv head)
+    int4* units;        // [8][cap] {t * 65536 + c, p, kv base low, kv base high | h << 24}
+    int cap;
+    int max_tok;
+    int max_tok_step;   // tokens of the step being launched (<= max_tok)
+};
+size_t attention_xcd_ints(int max_tok, int Hkv, int max_pos);
+AttnXcd attention_xcd_view(int32_t* base, int max_tok, int Hkv, int max_pos);
+// Checks once per process (a 64-workgroup launch and a copy) that workgroup i
+// runs on XCD i % 8; attention_xcd_merge is false until it has returned true.
+bool attention_xcd_probe();
 int launch_attention_rope(float* out, void* Kp, void* Vp, const float* part, int nsplit, int64_t split_stride,
                           int qkv_ld, const float* cs, const RowNorm& rn, const int32_t* tok_pos, int T, int Hq,
                           int Hkv, int HD, int64_t head_stride, int max_pos, float* po, float* pml, const Act16* act,
-                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool kv_f16);
+                          hipStream_t s, hipEvent_t ev_start, hipEvent_t ev_stop, bool kv_f16,
+                          const AttnXcd* xq = nullptr);
+// xq (optional): also fill the per-XCD queues (and reset their arrival
+// counts) for the decode tokens.
 int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_pos, const int32_t* tok2seq,
-                           const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s);
+                           const int64_t* kv_base, int T, int Hq, int max_pos, float* pml, hipStream_t s,
+                           const AttnXcd* xq = nullptr, int Hkv = 0);
+// Whether launch_attention_rope merges inside the attention kernel for this
+// shape (the per-XCD queues are needed then).
+bool attention_xcd_merge(int T, int Hq, int Hkv, int HD, int max_pos, bool has_act);
 size_t attention_partial_floats(int T, int Hq, int HD, int max_pos);
 int launch_attention_ragged(float* out, const float* q, const float* Kp, const float* Vp,
                             const int32_t* tok2seq, const int32_t* tok_pos, const int64_t* kv_base, int T,

@@ -360,6 +360,63 @@ def test_fused_rope_attention_equals_separate_kernels(switch_env):
         assert np.array_equal(Ka[:, :n], Kb[:, :n]) and np.array_equal(Va[:, :n], Vb[:, :n])
 
 
+XCD_SHAPE = LlamaShape(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, ffn=768, vocab=300, max_seq=1100)
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_decode_attention_merged_in_kernel_equals_merge_kernel(orc, switch_env, kv_f16):
+    """Decode steps (one token per sequence) of a shape whose kv head groups
+    fill whole 256-wide operand blocks (4 query heads of 128 per kv head)
+    merge the attention chunks inside the attention kernel, from per-XCD work
+    queues, instead of in a separate merge kernel (SLATE_HIP_ATTN_XCD=0).
+    Contexts of 1-1000 keys (up to four 256-key chunks per pair, pairs whose
+    last chunk holds one key), six sequences, three layers (each layer's
+    queues and arrival counts start from zero again), four decode steps: the
+    merge evaluates the same expressions in the same order, so logits and
+    K/V caches are bit-identical to the merge kernel's; the logits also
+    against the oracle (f32 caches)."""
+    switch_env.setenv("SLATE_HIP_KV_F16", "1" if kv_f16 else "0")
+    shape = XCD_SHAPE
+    t = make_llama(shape, 977, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(31)
+    lens = (1000, 300, 256, 40, 1, 511)
+    prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in lens]
+    runs = []
+    for xcd in ("1", "0"):
+        switch_env.setenv("SLATE_HIP_ATTN_XCD", xcd)
+        m = slate_amd.Llama.from_tensors(shape, t, max_slots=len(prompts), max_tokens=sum(lens))
+        sess = [m.session() for _ in prompts]
+        rc, lg, nxt = m.step(sess, list(lens), np.concatenate(prompts))
+        assert rc == 0
+        steps, feed = [], []
+        toks = np.asarray(nxt, np.int32)
+        for _ in range(4):
+            feed.append(toks)
+            rc, lg, nxt = m.step(sess, [1] * len(sess), toks)
+            assert rc == 0
+            steps.append(np.array(lg))
+            toks = np.asarray(nxt, np.int32)
+        runs.append((steps, feed, [s.kv() for s in sess]))
+        for s in sess:
+            s.free()
+        m.free()
+    (sa, fa, kva), (sb, fb, kvb) = runs
+    for k in range(4):
+        assert np.array_equal(fa[k], fb[k]) and np.array_equal(sa[k], sb[k]), k
+    for (Ka, Va), (Kb, Vb) in zip(kva, kvb):
+        assert np.array_equal(Ka, Kb) and np.array_equal(Va, Vb)
+    if kv_f16:
+        return
+    om = OracleModel(orc, shape, t)
+    for i, p in enumerate(prompts):
+        o = om.session()
+        rc, _ = o.prefill(p)
+        assert rc == 0
+        for k in range(4):
+            rc, want = o.decode(int(fa[k][i]))
+            assert rc == 0 and relerr(sa[k][i], want) < TOL, (i, k)
+
+
 def test_graph_replayed_decode_steps_match_eager_launches(golden):
     """Decode-only steps replay a captured HIP graph; interleaved with eager
     prompt steps and repeated many times, every replay gives bit-identical
@@ -569,7 +626,7 @@ SWITCHES = [("SLATE_HIP_FUSED_NORM", "0", "q4k"), ("SLATE_HIP_ATTN_MFMA", "0", "
             # the query-block prompt kernel: neither the MFMA nor the tokenwise path
             ("SLATE_HIP_ATTN_MFMA=0,SLATE_HIP_ATTN_TOKENWISE", "0", "q4k"),
             ("SLATE_HIP_ATTN_WAVE", "0", "q4k"), ("SLATE_HIP_ATTN_ROPE", "0", "q4k"),
-            ("SLATE_HIP_ATTN_ROPE", "2", "q4k"), ("SLATE_HIP_GRAPHS", "1", "q4k"),
+            ("SLATE_HIP_ATTN_ROPE", "2", "q4k"), ("SLATE_HIP_ATTN_XCD", "0", "q4k"), ("SLATE_HIP_GRAPHS", "1", "q4k"),
             ("SLATE_HIP_Q4K_R", "1", "q4k"), ("SLATE_HIP_Q4K_R", "4", "q4k"), ("SLATE_HIP_Q4K_W", "4", "q4k"),
             ("SLATE_HIP_Q4K_S", "1", "q4k"), ("SLATE_HIP_Q4K_S", "3", "q4k"), ("SLATE_HIP_Q4K_WGS", "64", "q4k"),
             ("SLATE_HIP_Q4K_PF_S", "3", "q4k"), ("SLATE_HIP_Q4K_DEC32", "0", "q4k"),
