@@ -382,7 +382,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--profile-steps", type=int, default=8, help="event-timed steps after the timed window")
+    ap.add_argument("--profile-steps", type=int, default=8,
+                    help="event-timed steps after the timed window (at least 1: the roofline comes from them)")
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--layers", type=int, default=None, help="layers (default: the shape's own)")
     ap.add_argument("--shape", choices=("8b", "70b"), default="8b",
@@ -397,6 +398,8 @@ def main():
                     help="run a 1 GiB device-to-device copy 5 times and exit")
     ap.add_argument("--ops", action="store_true", help="op-level Q4_K / Q8_0 matmul and ragged attention figures")
     args = ap.parse_args()
+    if args.profile_steps < 1:
+        ap.error("--profile-steps must be at least 1")
     if args.copy_calibration:
         import torch
         n = 1 << 28                                  # 2^28 f32 = 1 GiB each way
