@@ -190,7 +190,7 @@ __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restr
                                                           const int32_t* __restrict__ tok_pos,
                                                           const int32_t* __restrict__ tok2seq,
                                                           const int64_t* __restrict__ kv_base, int nch_max,
-                                                          int32_t* __restrict__ pairs) {
+                                                          int32_t* __restrict__ pairs, AttnXcd xq, int Hkv) {
     __shared__ int s_scan[1024];
     __shared__ int s_base;
     const int tid = threadIdx.x;
@@ -219,11 +219,24 @@ __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restr
         for (int c = 0; c < n; ++c)
             units[base + c] = make_int4(t * 65536 + c, p, (int)(uint32_t)((uint64_t)kvb & 0xffffffffu),
                                         (int)(uint32_t)((uint64_t)kvb >> 32));
+        if (xq.len && i < n_dec) {
+            // the per-XCD queues when Hkv % 8 == 0: pair (t, h) goes to queue
+            // h % 8, after Hkv / 8 pairs of every earlier token and the
+            // token's own heads h - 8, h - 16, ...
+            for (int h = 0; h < Hkv; ++h) {
+                int4* q = xq.units + (size_t)(h & 7) * xq.cap + (Hkv >> 3) * base + (h >> 3) * n;
+                for (int c = 0; c < n; ++c)
+                    q[c] = make_int4(t * 65536 + c, p, (int)(uint32_t)((uint64_t)kvb & 0xffffffffu),
+                                     (int)((uint32_t)((uint64_t)kvb >> 32) | ((uint32_t)h << 24)));
+                xq.arrive[t * Hkv + h] = 0;
+            }
+        }
         __syncthreads();
         if (tid == 1023) s_base += s_scan[1023];
         __syncthreads();
     }
     if (tid == 0) pairs[0] = s_base;
+    if (xq.len && tid < 8) xq.len[tid] = (Hkv >> 3) * s_base;
 }
 
 // Unit u of the list (both loads issued before either is used; u may lie
@@ -1115,7 +1128,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
         } else if (!prefill && (HD == 32 || HD == 64 || HD == 128)) {
             if (!pairs_ready) {
                 SH_LAUNCH(a.ev0, nullptr, attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos,
-                          tok2seq, kv_base, nch_max, pairs);
+                          tok2seq, kv_base, nch_max, pairs, AttnXcd{}, 0);
                 SH_CHECK_LAUNCH();
                 a.ev0 = nullptr;
             }
@@ -1319,15 +1332,17 @@ int launch_attention_pairs(const int32_t* dec_t0, int n_dec, const int32_t* tok_
         set_error(-5, "attention: %d query tokens / %d key chunks exceed the work-unit encoding", n_dec, nch_max);
         return -5;
     }
+    // every decode token's pairs must fit the queues and the arrival counts
+    if (xq && (Hkv <= 0 || Hkv > 127 || T > xq->max_tok)) {
+        set_error(-1, "attention: %d tokens x %d kv heads exceed the per-XCD queues", T, Hkv);
+        return -1;
+    }
+    // Hkv % 8 == 0: the pair list's own scan places every queue entry
+    const bool inline_q = xq && Hkv % 8 == 0;
     hipLaunchKernelGGL(attn_pairs_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, tok2seq, kv_base,
-                       nch_max, attn_unit_list(pml, T, Hq, nch_max));
+                       nch_max, attn_unit_list(pml, T, Hq, nch_max), inline_q ? *xq : AttnXcd{}, Hkv);
     SH_CHECK_LAUNCH();
-    if (xq) {
-        // every decode token's pairs must fit the queues and the arrival counts
-        if (Hkv <= 0 || Hkv > 127 || T > xq->max_tok) {
-            set_error(-1, "attention: %d tokens x %d kv heads exceed the per-XCD queues", T, Hkv);
-            return -1;
-        }
+    if (xq && !inline_q) {
         hipLaunchKernelGGL(attn_xcd_queues_kernel, dim3(1), dim3(1024), 0, s, dec_t0, n_dec, tok_pos, tok2seq,
                            kv_base, nch_max, Hkv, *xq);
         SH_CHECK_LAUNCH();

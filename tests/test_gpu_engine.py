@@ -361,22 +361,26 @@ def test_fused_rope_attention_equals_separate_kernels(switch_env):
 
 
 XCD_SHAPE = LlamaShape(n_layers=3, d_model=1024, n_heads=8, n_kv_heads=2, ffn=768, vocab=300, max_seq=1100)
+# 8 kv heads: the pair list's own scan fills the per-XCD queues
+XCD8_SHAPE = LlamaShape(n_layers=3, d_model=2048, n_heads=16, n_kv_heads=8, ffn=768, vocab=300, max_seq=1100)
 
 
-@pytest.mark.parametrize("kv_f16", [False, True])
-def test_decode_attention_merged_in_kernel_equals_merge_kernel(orc, switch_env, kv_f16):
-    """Decode steps (one token per sequence) of a shape whose kv head groups
-    fill whole 256-wide operand blocks (4 query heads of 128 per kv head)
-    merge the attention chunks inside the attention kernel, from per-XCD work
-    queues, instead of in a separate merge kernel (SLATE_HIP_ATTN_XCD=0).
-    Contexts of 1-1000 keys (up to four 256-key chunks per pair, pairs whose
-    last chunk holds one key), six sequences, three layers (each layer's
-    queues and arrival counts start from zero again), four decode steps: the
+@pytest.mark.parametrize("shape,kv_f16", [(XCD_SHAPE, False), (XCD_SHAPE, True), (XCD8_SHAPE, False)],
+                         ids=["hkv2", "hkv2_f16", "hkv8"])
+def test_decode_attention_merged_in_kernel_equals_merge_kernel(orc, switch_env, shape, kv_f16):
+    """Decode steps (one token per sequence) of shapes whose kv head groups
+    fill whole 256-wide operand blocks (4 or 2 query heads of 128 per kv
+    head; 2 kv heads: the queues' own kernel fills them, 8: the pair list's
+    scan does) merge the attention chunks inside the attention kernel, from
+    per-XCD work queues, instead of in a separate merge kernel
+    (SLATE_HIP_ATTN_XCD=0).  Contexts of 1-1000 keys (up to four 256-key
+    chunks per pair, pairs whose last chunk holds one key), six sequences,
+    three layers (each layer's arrival counts start from zero again), four
+    decode steps: the
     merge evaluates the same expressions in the same order, so logits and
     K/V caches are bit-identical to the merge kernel's; the logits also
     against the oracle (f32 caches)."""
     switch_env.setenv("SLATE_HIP_KV_F16", "1" if kv_f16 else "0")
-    shape = XCD_SHAPE
     t = make_llama(shape, 977, quant="q4k", output_quant="q4k")
     rng = np.random.default_rng(31)
     lens = (1000, 300, 256, 40, 1, 511)
