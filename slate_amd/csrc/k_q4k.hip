@@ -617,7 +617,6 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         // workgroup's set-up, staging prologue and partial stores), a last,
         // partly filled round costing a whole one (measured at T = 320: two
         // splits beat 8 and 14 on the 4096-row shapes by 8-14 %)
-        const int NT = act_tiles >= 4 ? 4 : 2;
         Q4kTargets tg{};
         int wgs = 0;
         for (int i = 0; i < n; ++i) {
@@ -629,14 +628,39 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         }
         tg.n = n;
         tg.grp_end = wgs;
-        const int tasks = wgs * ((act_tiles + NT - 1) / NT);
-        const int slots = pf_slots(NT);
-        int S = 1;
-        double best = 1e30;
-        for (int c = 1; c <= 16 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
-            const int rounds = (tasks * c + slots - 1) / slots;
-            const double cost = (double)rounds * ((double)(nblk + c - 1) / c + 4.0);
-            if (cost <= best + 1e-9) { best = cost; S = c; }   // ties: more splits (measured faster)
+        // split count for NT activation tiles per workgroup; *fill: how full
+        // the last round of workgroups is (1 when the rounds come out even),
+        // *nrounds: rounds of workgroups
+        auto plan = [&](int NT, double* fill, int* nrounds) {
+            const int tasks = wgs * ((act_tiles + NT - 1) / NT);
+            const int slots = pf_slots(NT);
+            int Sb = 1;
+            double best = 1e30;
+            for (int c = 1; c <= 16 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
+                const int rounds = (tasks * c + slots - 1) / slots;
+                const double cost = (double)rounds * ((double)(nblk + c - 1) / c + 4.0);
+                if (cost <= best + 1e-9) { best = cost; Sb = c; }   // ties: more splits (measured faster)
+            }
+            const int rem = tasks * Sb % slots;
+            *fill = rem ? (double)rem / slots : 1.0;
+            *nrounds = (tasks * Sb + slots - 1) / slots;
+            return Sb;
+        };
+        // four activation tiles per workgroup (one workgroup per CU: its two
+        // operand buffers take 147 KiB of LDS), or two (two per CU) when the
+        // four-tile plan runs two or more rounds of workgroups and leaves the
+        // last under 60 % full: half-size workgroups fill that round better
+        // (gate+up 2x14336x4096 at 320 rows 184 vs 202 us, 512 rows 269 vs
+        // 280 us; 70B gate+up at 384 rows 799 vs 810 us) and are 1-7 % slower
+        // where the rounds come out even or one round holds everything (every
+        // other 8B and 70B shape measured at 96-1024 rows)
+        double fill = 1.0;
+        int rounds = 1;
+        int NT = act_tiles >= 4 ? 4 : 2;
+        int S = plan(NT, &fill, &rounds);
+        if (NT == 4 && rounds >= 2 && fill < 0.6) {
+            NT = 2;
+            S = plan(2, &fill, &rounds);
         }
         const int S_env = knobs().q4k_pf_s;
         if (S_env > 0) S = std::min(S_env, std::max(1, std::min(max_splits, nblk)));
