@@ -13,6 +13,7 @@
 // combines the chunks with log-sum-exp rescaling.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "launch.h"
 #include "act16.h"
@@ -843,10 +844,23 @@ __global__ void xcc_probe_kernel(int32_t* out) {
 static int device_cus();
 
 // Whether workgroup i of a launch runs on XCD i % 8 of an eight-XCD device
-// (read from the hardware register by 64 workgroups), once per process.
-static std::atomic<int> g_xcd_rr{-1};
+// (read from the hardware register by 64 workgroups), once per device and
+// process; -1: not probed yet.
+constexpr int XCD_MAX_DEVICES = 64;
+static std::atomic<int> g_xcd_rr[XCD_MAX_DEVICES];
+static std::once_flag g_xcd_init;
+static std::atomic<int>* xcd_flag() {
+    std::call_once(g_xcd_init, [] {
+        for (auto& f : g_xcd_rr) f.store(-1);
+    });
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= XCD_MAX_DEVICES) return nullptr;
+    return &g_xcd_rr[dev];
+}
 bool attention_xcd_probe() {
-    int v = g_xcd_rr.load();
+    std::atomic<int>* f = xcd_flag();
+    if (!f) return false;
+    int v = f->load();
     if (v >= 0) return v == 1;
     bool ok = device_cus() == 256;
     int32_t* d = nullptr;
@@ -858,7 +872,7 @@ bool attention_xcd_probe() {
         (void)hipFree(d);
     }
     for (int i = 0; ok && i < 64; ++i) ok = (h[i] & 15) == i % 8;
-    g_xcd_rr.store(ok ? 1 : 0);
+    f->store(ok ? 1 : 0);
     return ok;
 }
 
@@ -1204,15 +1218,12 @@ static int launch_rope_hd(int G, bool f16, dim3 grid, hipStream_t s, hipEvent_t 
     }
 }
 
-// Compute units of the device (for persistent grids).
+// Compute units of the current device (256 if the query fails).
 static int device_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-    }
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
     return cus;
 }
 
@@ -1220,7 +1231,10 @@ bool attention_xcd_merge(int T, int Hq, int Hkv, int HD, int max_pos, bool has_a
     (void)has_act;
     // workgroup i on XCD i % 8, as probed (attention_xcd_probe) for this device
     if (!knobs().attn_xcd || rope_fused() != 1 || !wave_kernel() || T <= 0 || T > ATT_WAVE_MAX_TOKENS ||
-        Hkv <= 0 || Hq % Hkv != 0 || g_xcd_rr.load() != 1)
+        Hkv <= 0 || Hq % Hkv != 0)
+        return false;
+    const std::atomic<int>* f = xcd_flag();
+    if (!f || f->load() != 1)
         return false;
     const int G = Hq / Hkv;
     if (!(HD == 32 || HD == 64 || HD == 128) || G * HD > 512 || (G * HD) % 256 != 0) return false;
