@@ -421,6 +421,36 @@ def test_decode_attention_merged_in_kernel_equals_merge_kernel(orc, switch_env, 
             assert rc == 0 and relerr(sa[k][i], want) < TOL, (i, k)
 
 
+@pytest.mark.parametrize("nseq", [64, 65])
+def test_decode_attention_in_kernel_merge_at_the_batch_limit(switch_env, nseq):
+    """The in-kernel merge takes decode steps of up to 64 sequences (64: the
+    largest grid and the fullest queues; 65: the merge kernel takes over):
+    ragged contexts of 1-700 keys, 8 kv heads, two decode steps, logits and
+    next tokens bit-identical to the merge kernel's (SLATE_HIP_ATTN_XCD=0)."""
+    t = make_llama(XCD8_SHAPE, 4242, quant="q4k", output_quant="q4k")
+    rng = np.random.default_rng(nseq)
+    lens = [int(n) for n in rng.integers(1, 700, nseq)]
+    prompts = [rng.integers(0, XCD8_SHAPE.vocab, n).astype(np.int32) for n in lens]
+    runs = []
+    for xcd in ("1", "0"):
+        switch_env.setenv("SLATE_HIP_ATTN_XCD", xcd)
+        m = slate_amd.Llama.from_tensors(XCD8_SHAPE, t, max_slots=nseq, max_tokens=sum(lens))
+        sess = [m.session() for _ in prompts]
+        rc, lg, nxt = m.step(sess, lens, np.concatenate(prompts))
+        assert rc == 0
+        out = []
+        for _ in range(2):
+            rc, lg, nxt = m.step(sess, [1] * nseq, np.asarray(nxt, np.int32))
+            assert rc == 0
+            out.append((np.array(lg), np.array(nxt)))
+        for s_ in sess:
+            s_.free()
+        m.free()
+        runs.append(out)
+    for (la, na), (lb, nb) in zip(*runs):
+        assert np.array_equal(la, lb) and np.array_equal(na, nb)
+
+
 def test_graph_replayed_decode_steps_match_eager_launches(golden):
     """Decode-only steps replay a captured HIP graph; interleaved with eager
     prompt steps and repeated many times, every replay gives bit-identical
