@@ -4,8 +4,9 @@
   in C11 and C++, with slate's factories (backend.h:104-110) and the HIP
   one both declared;
 * the loader binding slate_amd/bind/slate_llama_to_hip.c, whose text is the
-  block INTEGRATION.md shows, compiles against slate's llama.h with its
-  struct-layout asserts, and the built binding library exports it.
+  C block of the integration guide's LLaMA section, compiles against slate's
+  llama.h with its struct-layout asserts, and the built binding library
+  exports it.
 """
 import os
 import re
