@@ -14,7 +14,8 @@ greedy tokens equal unless the reference's top-2 gap is below that.  The
 reference feeds the GPU's first greedy token into its second step, so the
 second step also compares the reference's own K/V append with the GPU's.
 One sequence prefilled and decoded alone gets the logits it gets in the
-batch (within 1e-4)."""
+batch (within 1e-4), and the whole run repeated in fresh sessions gets the
+same bits."""
 import os
 from concurrent.futures import ThreadPoolExecutor
 
@@ -138,6 +139,18 @@ def test_8b_full_size_decode_matches_reference():
         rc, l1 = solo.decode(tok)
         assert rc == 0 and relerr(l1, lg[0]) < 1e-4
     solo.free()
+    for s in sess:
+        s.free()
+    # run to run: the same prompts and steps in fresh sessions give the same
+    # bits (every reduction of the path runs in a fixed order; the decode
+    # attention's arrival counts only pick which unit merges)
+    sess = [m.session() for _ in range(NSEQ)]
+    assert prefill_ragged(m, sess, prompts) == toks0
+    rc, r1, n1 = m.step(sess, [1] * NSEQ, np.asarray(toks0, np.int32))
+    assert rc == 0
+    rc, r2, n2 = m.step(sess, [1] * NSEQ, n1)
+    assert rc == 0
+    assert np.array_equal(r1, lg1) and np.array_equal(r2, lg2) and np.array_equal(n2, nx2)
     for s in sess:
         s.free()
     m.free()
