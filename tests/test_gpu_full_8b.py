@@ -13,9 +13,11 @@ not built, against the oracle's restatement of it: normwise rel 1e-3, and
 greedy tokens equal unless the reference's top-2 gap is below that.  The
 reference feeds the GPU's first greedy token into its second step, so the
 second step also compares the reference's own K/V append with the GPU's.
-One sequence prefilled and decoded alone gets the logits it gets in the
-batch (within 1e-4), and the whole run repeated in fresh sessions gets the
-same bits."""
+A third, mixed step (the decode tokens beside a new sequence's 300-token
+prompt, all rows on the prompt kernels) is checked the same way, and the new
+sequence's logits against its prompt prefilled alone (1e-4).  One sequence
+prefilled and decoded alone gets the logits it gets in the batch (within
+1e-4), and the whole run repeated in fresh sessions gets the same bits."""
 import os
 from concurrent.futures import ThreadPoolExecutor
 
@@ -111,7 +113,7 @@ class Reference:
 
 
 def test_8b_full_size_decode_matches_reference():
-    m = slate_amd.Llama.synthetic(SHAPE, seed=2026, quant=18, max_slots=NSEQ + 1, max_tokens=MAX_TOKENS)
+    m = slate_amd.Llama.synthetic(SHAPE, seed=2026, quant=18, max_slots=NSEQ + 2, max_tokens=MAX_TOKENS)
     rng = np.random.default_rng(0xC4)
     prompts = [rng.integers(0, SHAPE.vocab, n).astype(np.int32) for n in rng.integers(128, 2049, NSEQ)]
     sess = [m.session() for _ in range(NSEQ)]
@@ -129,6 +131,21 @@ def test_8b_full_size_decode_matches_reference():
                 assert relerr(lg[i], want[i]) < TOL, (k, i, relerr(lg[i], want[i]))
                 assert int(nx[i]) == int(np.argmax(lg[i]))
                 assert int(nx[i]) == int(np.argmax(want[i])) or not gap_ok(want[i]), (k, i)
+        # a mixed step, as an arrival makes one: the 16 decode tokens ride with
+        # a new sequence's 300-token prompt (every row on the prompt kernels)
+        arrival = rng.integers(0, SHAPE.vocab, 300).astype(np.int32)
+        new = m.session()
+        rc, lg3, nx3 = m.step(sess + [new], [1] * NSEQ + [len(arrival)], np.concatenate([nx2, arrival]))
+        assert rc == 0 and np.all(np.isfinite(lg3))
+        want = ref.decode(nx2)
+        for i in range(NSEQ):
+            assert relerr(lg3[i], want[i]) < TOL, (i, relerr(lg3[i], want[i]))
+            assert int(nx3[i]) == int(np.argmax(want[i])) or not gap_ok(want[i]), i
+        alone = m.session()
+        rc, la = alone.prefill(arrival)
+        assert rc == 0 and relerr(lg3[NSEQ], la) < 1e-4
+        alone.free()
+        new.free()
     finally:
         ref.close()
     # batch invariance: the first sequence alone
