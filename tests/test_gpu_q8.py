@@ -167,6 +167,27 @@ def test_matmul_q8_0_tiled(hip, orc, M, K, B):
         assert relerr(got, orc.q8_0_matmul(raw, X, M, K)) < 1e-5
 
 
+@pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 14336)])
+def test_matmul_q8_0_c2_shapes(hip, orc, M, K):
+    """Q8_0 at the Q4_K op's full sizes: W ~ N(0, 0.02) quantised to Q8_0, X ~
+    N(0, 1), B in {1, 4, 16, 64} (decode plan and prompt kernel), row and
+    tiled layouts bit-identical, against the oracle's Q8_0 matvec
+    (quant.c:64-133) at rel 1e-5."""
+    rng, raw = q8_case(M, K, M + 5 * K)
+    Wd = dev(raw)
+    T = DB(hip.lib.slate_hip_q8_0_tiled_bytes(M, K))
+    check(hip.lib.slate_hip_q8_0_tile(T.p, Wd.p, M, K), "q8_0_tile")
+    for B in (1, 4, 16, 64):
+        X = rng.normal(0, 1, (B, K)).astype(np.float32)
+        Xd = dev(X)
+        Yr, Yt = DB(B * M * 4), DB(B * M * 4)
+        check(hip.lib.slate_hip_matmul_q8_0(Yr.p, Wd.p, Xd.p, B, M, K), "matmul_q8_0")
+        check(hip.lib.slate_hip_matmul_q8_0_tiled(Yt.p, T.p, Xd.p, B, M, K), "matmul_q8_0_tiled")
+        got, gt = Yr.to_array(np.float32, (B, M)), Yt.to_array(np.float32, (B, M))
+        assert np.array_equal(bits(got), bits(gt)), B
+        assert relerr(got, orc.q8_0_matmul(raw, X, M, K)) < 1e-5, B
+
+
 def test_matmul_q8_0_rejects_bad_shapes(hip):
     hip.lib.slate_hip_clear_error()
     Y, A, X = DB(64), DB(64), DB(64)
