@@ -270,6 +270,14 @@ __device__ __forceinline__ float4 ld_kv4(const _Float16* p) {
     const kv_half2_t a = __builtin_bit_cast(kv_half2_t, r.x), b = __builtin_bit_cast(kv_half2_t, r.y);
     return make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
 }
+// Eight f16 K/V values (16 bytes) as two float4: elements 0-3 and 4-7.
+__device__ __forceinline__ void ld_kv8(const _Float16* p, float4& lo, float4& hi) {
+    const uint4 r = *(const uint4*)p;
+    const kv_half2_t a = __builtin_bit_cast(kv_half2_t, r.x), b = __builtin_bit_cast(kv_half2_t, r.y);
+    const kv_half2_t c = __builtin_bit_cast(kv_half2_t, r.z), d = __builtin_bit_cast(kv_half2_t, r.w);
+    lo = make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+    hi = make_float4((float)c.x, (float)c.y, (float)d.x, (float)d.y);
+}
 
 // Decode steps in which every sequence adds one token: the attention unit
 // also does what rope_kv_kernel does for its token and kv head, from the
@@ -533,6 +541,20 @@ __device__ __forceinline__ void attn_dec_wave_unit(
     const KVT* Kh = Kp + base;
     const KVT* Vh = Vp + base;
     const int kw0 = wv * KW;
+    // dims of a row that lane ls holds, as NV float4: f32 rows 32i + 4ls ..
+    // +3 (one 16-byte load each); f16 rows (head_dim 64 / 128) in pairs,
+    // 64(i/2) + 8ls + 4(i%2) .. +3, so that one 16-byte load brings two
+    constexpr bool W16 = sizeof(KVT) == 2 && NV % 2 == 0;
+    auto dof = [&](int i) { return W16 ? 64 * (i >> 1) + 8 * ls + 4 * (i & 1) : 32 * i + 4 * ls; };
+    auto ld_row = [&](const KVT* row, float4 (&dst)[NV]) {
+        if constexpr (W16) {
+#pragma unroll
+            for (int i = 0; i < NV; i += 2) ld_kv8((const _Float16*)row + dof(i), dst[i], dst[i + 1]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) dst[i] = ld_kv4(row + dof(i));
+        }
+    };
     // with ROPE, the first KP rounds of key rows are loaded before the
     // prologue where the chunk does not hold key p (its rows are final), so
     // that their latency overlaps the prologue's
@@ -543,8 +565,7 @@ __device__ __forceinline__ void attn_dec_wave_unit(
 #pragma unroll
             for (int it = 0; it < KP; ++it) {
                 const KVT* kr = Kh + (int64_t)min(kw0 + 8 * it + lg, nk - 1) * HD;
-#pragma unroll
-                for (int i = 0; i < NV; ++i) kpre[it][i] = ld_kv4(kr + 32 * i + 4 * ls);
+                ld_row(kr, kpre[it]);
             }
         }
     };
@@ -565,16 +586,19 @@ __device__ __forceinline__ void attn_dec_wave_unit(
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int i = 0; i < NV; ++i)
-                qv[gi][i] = ROPE ? *(const float4*)(&s_q[gi][32 * i + 4 * ls])
-                                 : *(const float4*)(qt + gi * HD + 32 * i + 4 * ls);
+                qv[gi][i] = ROPE ? *(const float4*)(&s_q[gi][dof(i)]) : *(const float4*)(qt + gi * HD + dof(i));
         float sc[G][IT];
 #pragma unroll
         for (int it = 0; it < IT; ++it) {
             const int j = kw0 + 8 * it + lg;
             const KVT* kr = Kh + (int64_t)min(j, nk - 1) * HD;   // clamped: stays inside the token's keys
             float4 kv[NV];
+            if (it < KP) {
 #pragma unroll
-            for (int i = 0; i < NV; ++i) kv[i] = it < KP ? kpre[it][i] : ld_kv4(kr + 32 * i + 4 * ls);
+                for (int i = 0; i < NV; ++i) kv[i] = kpre[it < KP ? it : 0][i];
+            } else {
+                ld_row(kr, kv);
+            }
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 float a = 0.f;
@@ -596,8 +620,7 @@ __device__ __forceinline__ void attn_dec_wave_unit(
 #pragma unroll
         for (int it = 0; it < VP; ++it) {
             const KVT* vr = Vh + (int64_t)min(kw0 + 8 * it + lg, nk - 1) * HD;
-#pragma unroll
-            for (int i = 0; i < NV; ++i) vpre[it][i] = ld_kv4(vr + 32 * i + 4 * ls);
+            ld_row(vr, vpre[it]);
         }
         __builtin_amdgcn_sched_barrier(0);
         float mx[G], sum[G];
@@ -626,8 +649,12 @@ __device__ __forceinline__ void attn_dec_wave_unit(
             const int j = kw0 + 8 * it + lg;
             const KVT* vr = Vh + (int64_t)min(j, nk - 1) * HD;
             float4 vv[NV];
+            if (it < VP) {
 #pragma unroll
-            for (int i = 0; i < NV; ++i) vv[i] = it < VP ? vpre[it][i] : ld_kv4(vr + 32 * i + 4 * ls);
+                for (int i = 0; i < NV; ++i) vv[i] = vpre[it < VP ? it : 0][i];
+            } else {
+                ld_row(vr, vv);
+            }
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
                 const float pj = sc[gi][it];
@@ -654,7 +681,7 @@ __device__ __forceinline__ void attn_dec_wave_unit(
 #pragma unroll
             for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-                for (int i = 0; i < NV; ++i) s_o[wv][lane >> 4][gi][8 * i + ls] = acc[gi][i];
+                for (int i = 0; i < NV; ++i) s_o[wv][lane >> 4][gi][dof(i) >> 2] = acc[gi][i];
         if (lane == 0)
 #pragma unroll
             for (int gi = 0; gi < G; ++gi) {
