@@ -8,10 +8,12 @@ contexts prefilled to U[128, 2048] tokens (untimed); each sequence stops
 after U[32, 256] generated tokens and its slot is taken by a new arrival
 whose U[64, 512]-token prompt is prefilled inside the next ragged step
 (mixed prefill + decode).  The workload starts in steady state: after the
-context prefill each sequence's generated count is drawn uniformly from
-[0, stop), so sequences finish and arrivals come at the steady rate from
-the first timed step on.  A step = one pass of the engine over the packed
-batch; each step produces one token per sequence.
+context prefill each sequence is placed at a point of its generation drawn
+from the stop-and-replace process's equilibrium law, stratified over the
+sequences, so every window of n steps holds about n * B / E[stop] arrivals
+(prompts prefilled in mixed steps) from the first timed step on.  A step =
+one pass of the engine over the packed batch; each step produces one token
+per sequence.
 
 Printed: one JSON line.  value = generated tokens / wall time over the K
 timed steps (weights and KV resident in HBM; each step's descriptor upload
@@ -101,7 +103,9 @@ class Workload:
         self.last = [0] * B            # last generated token
         self.gen = [0] * B
         self.stop = [0] * B
-        self.arrivals = 0
+        self.arrivals = 0              # sequences replaced (their prompt goes into the next step)
+        self.prompts = 0               # prompts prefilled inside steps
+        self.prompt_tokens = 0
 
     def new_prompt(self, lo, hi):
         n = int(self.rng.integers(lo, hi + 1))
@@ -115,16 +119,35 @@ class Workload:
         self.gen[i] = 0
         self.stop[i] = int(self.rng.integers(32, 257))
 
+    def steady_state_positions(self):
+        """(stop, generated) per slot at the steady state of the
+        stop-and-replace process, stratified over the slots.  A slot's
+        remaining tokens R = stop - generated follow the equilibrium
+        residual-life law of stop ~ U[32, 256] with generated >= 1:
+        P(R = r) proportional to P(stop > r), r = 1 .. 255.  The B slots
+        take the R quantiles (k + u0) / B, k = 0 .. B-1, for one uniform u0,
+        in random order (systematic sampling: every window of n steps holds
+        about n * B / E[stop] finishing sequences, as a long-running server
+        sees, instead of whatever one seed gives); then stop ~ U[max(32,
+        R + 1), 256] (the law of stop given R) and generated = stop - R."""
+        lo, hi = 32, 256
+        r = np.arange(1, hi)
+        w = np.where(r < lo, 1.0, (hi - r) / (hi - lo + 1.0))   # P(stop > r)
+        cdf = np.cumsum(w) / w.sum()
+        u = (np.arange(self.B) + self.rng.random()) / self.B
+        R = r[np.minimum(np.searchsorted(cdf, u, side="right"), len(r) - 1)]
+        R = R[self.rng.permutation(self.B)]
+        stop = np.array([int(self.rng.integers(max(lo, x + 1), hi + 1)) for x in R])
+        return stop, stop - R
+
     def prefill_all(self):
         """Untimed: initial contexts U[128, 2048], packed several per step;
         then each sequence is placed where the steady state of the
-        stop-and-replace process puts it: a slot is found in a sequence of
-        length L with probability proportional to L (length-biased stop), at
-        a uniform point of its generation (gen ~ U[1, stop))."""
-        lens = np.arange(32, 257)
+        stop-and-replace process puts it (steady_state_positions)."""
+        stop, gen = self.steady_state_positions()
         for i in range(self.B):
             self.start(i, self.new_prompt(128, 2048))
-            self.stop[i] = int(self.rng.choice(lens, p=lens / lens.sum()))
+            self.stop[i] = int(stop[i])
         todo = list(range(self.B))
         while todo:
             group, T = [], 0
@@ -139,7 +162,7 @@ class Workload:
             for i, t in zip(group, nxt):
                 self.pending[i] = None
                 self.last[i] = int(t)
-                self.gen[i] = 1 + int(self.rng.integers(0, self.stop[i] - 1))
+                self.gen[i] = int(gen[i])
 
     def step(self, want_logits=False):
         """One ragged step; returns (mixed, logits, pos0, n_new)."""
@@ -153,6 +176,8 @@ class Workload:
                 n_new.append(1)
                 toks.append(np.array([self.last[i]], np.int32))
         mixed = any(n > 1 for n in n_new)
+        self.prompts += sum(1 for n in n_new if n > 1)
+        self.prompt_tokens += sum(n for n in n_new if n > 1)
         rc, lg, nxt = self.m.step(self.sess, n_new, np.concatenate(toks), want_logits=want_logits)
         assert rc == 0, f"step rc={rc}"
         for i in range(self.B):
@@ -181,7 +206,7 @@ def run_c4(args, shape):
         wl.step()
     lib = slate_amd.load_library()
     lib.slate_hip_sync()
-    arrivals0 = wl.arrivals
+    prompts0, ptok0 = wl.prompts, wl.prompt_tokens
     step_s, step_mixed, step_by, step_tok = [], [], [], []
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -193,7 +218,8 @@ def run_c4(args, shape):
         step_tok.append(args.batch)
     lib.slate_hip_sync()
     dt = time.perf_counter() - t0
-    arrivals = wl.arrivals - arrivals0
+    arrivals = wl.prompts - prompts0          # prompts prefilled inside the timed steps
+    prompt_tokens = wl.prompt_tokens - ptok0
     tokens = int(sum(step_tok))
     value = tokens / dt
     dec = [i for i, mx in enumerate(step_mixed) if not mx]
@@ -202,7 +228,8 @@ def run_c4(args, shape):
     step_frac = sum(step_by) / dt / (HBM_PEAK_GBS * 1e9)
     dec_frac = sum(step_by[i] for i in dec) / dec_s / (HBM_PEAK_GBS * 1e9) if dec else None
     mix_ms = [round(1e3 * t, 1) for t, mx in zip(step_s, step_mixed) if mx]
-    log(f"{args.steps} steps in {dt:.3f} s, {sum(step_mixed)} mixed ({arrivals} arrivals); decode-only steps "
+    log(f"{args.steps} steps in {dt:.3f} s, {sum(step_mixed)} mixed ({arrivals} prompts, {prompt_tokens} prompt "
+        f"tokens); decode-only steps "
         f"{1e3 * np.median([step_s[i] for i in dec]) if dec else 0:.2f} ms median; mixed steps {mix_ms} ms; "
         f"step_frac {step_frac:.3f}, decode_step_frac {dec_frac if dec_frac is None else round(dec_frac, 3)}")
     # kernel-class timing in its own window (events recorded by every dispatch)
@@ -242,6 +269,7 @@ def run_c4(args, shape):
                    "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "q4_k", "kv_cache": "f16" if lib.slate_hip_llama_kv_f16(m.h) == 1 else "f32",
                    "batch": args.batch, "mixed_prefill_steps": int(sum(step_mixed)), "arrivals": arrivals,
+                   "prompt_tokens": prompt_tokens,
                    "mean_context_start": round(float(np.mean(ctx0)), 1)},
         "decode_only_tok_s": None if dec_tok_s is None else round(dec_tok_s, 1),
         "roofline": roofline,

@@ -293,7 +293,10 @@ int   slate_hip_llama_profile(slate_hip_llama_t* m, int enable);
 /* graphs(m, 1) (or SLATE_HIP_GRAPHS=1): decode-only steps (one token per
  * session) are captured once per batch size into a HIP graph and replayed.
  * Default off: every kernel is launched separately.  Same results either
- * way.  No slate counterpart (slate has no device graphs). */
+ * way.  Refused (-5, graphs stay off) while a rocprofiler tool is attached
+ * (ROCPROF* / ROCP_* in the environment): a graph launch under
+ * rocprofv3 --kernel-trace has ended in a crash inside the HIP runtime.
+ * No slate counterpart (slate has no device graphs). */
 int   slate_hip_llama_graphs(slate_hip_llama_t* m, int enable);
 /* 1 when the engine keeps its K/V cache in f16 (opt-in at creation with
  * SLATE_HIP_KV_F16=1, head_dim 32/64/128), 0 for f32 as the reference
@@ -301,6 +304,15 @@ int   slate_hip_llama_graphs(slate_hip_llama_t* m, int enable);
  * cached element to 11 bits, a numerics change measured against the parity
  * tolerance.  slate_hip_llama_session_kv returns f32 either way. */
 int   slate_hip_llama_kv_f16(const slate_hip_llama_t* m);
+/* 1 while the engine's decode steps merge the attention chunks inside the
+ * decode attention kernel (workgroup i takes its work from a queue of XCD
+ * i % 8 and the merging unit reads the partials from that XCD's L2), 0 when
+ * they use the separate merge kernel: shapes the in-kernel merge does not
+ * take, SLATE_HIP_ATTN_XCD=0, a device where the placement probe failed, or
+ * after a launch reported a workgroup on another XCD (the engine then runs
+ * that step again on the merge kernel and keeps to it).  No slate
+ * counterpart. */
+int   slate_hip_llama_attn_xcd_merge(const slate_hip_llama_t* m);
 int   slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes,
                                    int64_t* launches);
 

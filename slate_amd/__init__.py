@@ -116,6 +116,7 @@ SIGNATURES = {
     "slate_hip_llama_profile": (C.c_int, [vp, C.c_int]),
     "slate_hip_llama_graphs": (C.c_int, [vp, C.c_int]),
     "slate_hip_llama_kv_f16": (C.c_int, [vp]),
+    "slate_hip_llama_attn_xcd_merge": (C.c_int, [vp]),
     "slate_hip_llama_profile_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double),
                                                C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
 }

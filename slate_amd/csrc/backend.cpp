@@ -106,18 +106,20 @@ hipStream_t stream() { return ensure() ? g_stream : nullptr; }
 
 static Knobs g_knobs;
 static std::once_flag g_knobs_once;
+static thread_local const Knobs* t_knobs = nullptr;
 
 static int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     return v ? atoi(v) : dflt;
 }
 
-void reload_knobs() {
+Knobs read_knobs() {
     Knobs k;
     k.attn_wave = env_int("SLATE_HIP_ATTN_WAVE", 1) != 0;
     k.attn_rope = env_int("SLATE_HIP_ATTN_ROPE", 1);
     if (k.attn_rope != 0 && k.attn_rope != 2) k.attn_rope = 1;
     k.attn_xcd = env_int("SLATE_HIP_ATTN_XCD", 1) != 0;
+    k.attn_xcd_rot = env_int("SLATE_HIP_ATTN_XCD_ROT", 0) & 7;
     k.attn_mfma = std::min(2, std::max(0, env_int("SLATE_HIP_ATTN_MFMA", 1)));
     k.q4k_w = env_int("SLATE_HIP_Q4K_W", 8) == 4 ? 4 : 8;
     k.q4k_r = env_int("SLATE_HIP_Q4K_R", 0);
@@ -130,13 +132,17 @@ void reload_knobs() {
     if (k.q8_r != 1 && k.q8_r != 2 && k.q8_r != 4) k.q8_r = 0;
     k.q8_s = std::max(0, env_int("SLATE_HIP_Q8_S", 0));
     k.q8_wgs = std::max(1, env_int("SLATE_HIP_Q8_WGS", 448));
-    g_knobs = k;
+    return k;
 }
 
 const Knobs& knobs() {
-    std::call_once(g_knobs_once, reload_knobs);
+    if (t_knobs) return *t_knobs;
+    std::call_once(g_knobs_once, [] { g_knobs = read_knobs(); });
     return g_knobs;
 }
+
+KnobScope::KnobScope(const Knobs* k) : prev_(t_knobs) { t_knobs = k; }
+KnobScope::~KnobScope() { t_knobs = prev_; }
 
 // Serialises multi-kernel entry sequences that share scratch buffers.
 std::mutex g_enqueue_mu;

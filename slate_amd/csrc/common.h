@@ -47,15 +47,21 @@ bool device_ok();            // a gfx950 device was opened
             hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                  \
     } while (0)
 
-// Plan and path switches (SLATE_HIP_* environment variables), read when the
-// library initialises and again whenever an engine is created
-// (reload_knobs), so one process can build engines under different settings.
-// The defaults are the measured fastest at the reference's numerics; every
-// setting gives results within the parity tolerances.
+// Plan and path switches (SLATE_HIP_* environment variables).  The C ABI's
+// entries use the process defaults, read once when the library initialises;
+// an engine reads its own copy when it is created (read_knobs) and every
+// step it enqueues uses that copy (KnobScope on the enqueuing thread), so
+// engines built under different settings keep their own kernel paths and a
+// new engine never changes an existing one's.  The defaults are the measured
+// fastest at the reference's numerics; every setting gives results within
+// the parity tolerances.
 struct Knobs {
     int attn_wave = 1;     // SLATE_HIP_ATTN_WAVE=0: phased decode attention for every shape
     int attn_rope = 1;     // SLATE_HIP_ATTN_ROPE: 0 RoPE/append in their own kernel, 2 fused into the phased kernel
     int attn_xcd = 1;      // SLATE_HIP_ATTN_XCD=0: decode attention partials merged by their own kernel
+    int attn_xcd_rot = 0;  // SLATE_HIP_ATTN_XCD_ROT=r (tests): the placement check of the in-kernel merge
+                           // expects workgroup i on XCD (i + r) % 8, so r != 0 makes every launch report a
+                           // misplacement and exercises the engine's fallback
     int attn_mfma = 1;     // SLATE_HIP_ATTN_MFMA: prompt blocks on the MFMA kernel 0 never, 1 when the
                            // step's prompt work outweighs its decode work, 2 whenever a step has prompt chunks
     int q4k_w = 8;         // SLATE_HIP_Q4K_W: waves per decode workgroup (4 or 8)
@@ -68,8 +74,21 @@ struct Knobs {
     int q8_s = 0;
     int q8_wgs = 448;
 };
+// The switches in force on this thread: the enclosing KnobScope's, else the
+// process defaults.
 const Knobs& knobs();
-void reload_knobs();
+// The switches as the environment sets them now.
+Knobs read_knobs();
+class KnobScope {
+  public:
+    explicit KnobScope(const Knobs* k);
+    ~KnobScope();
+    KnobScope(const KnobScope&) = delete;
+    KnobScope& operator=(const KnobScope&) = delete;
+
+  private:
+    const Knobs* prev_;
+};
 
 // Scratch owned by the backend: grown on demand, reused across calls.  Every
 // use happens on the single backend stream, so reuse is ordered.

@@ -16,6 +16,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <mutex>
@@ -96,6 +97,10 @@ struct slate_hip_llama {
     int n_dec = 0, n_pre = 0;
     bool step_mixed = false;       // the step carries a prompt chunk (profiling classes)
     bool step_one_each = false;    // every sequence of the step adds exactly one token
+    Knobs knobs;                   // kernel-path switches, read at creation (every step runs under them)
+    // The decode attention's in-kernel merge is turned off for this engine
+    // once a launch reported a workgroup on another XCD than its queue's.
+    bool xcd_off = false;
     float* h_logits = nullptr;
     std::vector<int> free_slots;
     std::vector<void*> allocs;
@@ -155,6 +160,16 @@ bool valid_cfg(const slate_hip_llama_config_t* c) {
            c->n_heads * c->head_dim == c->d_model && c->max_seq > 0 && c->vocab > 0;
 }
 
+// Whether a rocprofiler tool is attached to the process (rocprofv3 passes
+// its options as ROCPROF* / ROCP_* variables).  Graph replay stays off then:
+// a graph launch under rocprofv3 --kernel-trace has ended in a crash inside
+// the HIP runtime, with no cause found in this library.
+bool tracer_attached() {
+    for (char** e = environ; e && *e; ++e)
+        if (strncmp(*e, "ROCPROF", 7) == 0 || strncmp(*e, "ROCP_", 5) == 0) return true;
+    return false;
+}
+
 // Allocate everything but the weights.
 int alloc_runtime(slate_hip_llama* m) {
     const auto& c = m->cfg;
@@ -212,7 +227,8 @@ int alloc_runtime(slate_hip_llama* m) {
     m->defer_norm = getenv("SLATE_HIP_FUSED_NORM") == nullptr || atoi(getenv("SLATE_HIP_FUSED_NORM")) != 0;
     // opt-in: at 8B shapes a decode step is not launch-bound (graph replay
     // measured 3.37 ms per B=16 step against 3.35 ms launched eagerly)
-    m->graphs_on = getenv("SLATE_HIP_GRAPHS") != nullptr && atoi(getenv("SLATE_HIP_GRAPHS")) != 0;
+    m->graphs_on = getenv("SLATE_HIP_GRAPHS") != nullptr && atoi(getenv("SLATE_HIP_GRAPHS")) != 0 &&
+                   !tracer_attached();
     // prompt-chunk tokens attend through the decode kernel (one query token
     // per work unit, whole coalesced K/V rows; the shared prefix re-reads
     // hit L2), which beats the query-block kernel for these head sizes; the
@@ -533,9 +549,13 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if ((rc = launch_embed_rows(m->x, m->tok_embd, m->d_tok, T, c.vocab, D, s))) return rc;
     // the decode attention work units depend only on positions: once per step
     AttnXcd xq{};
-    const bool xcd = m->step_one_each && T <= m->max_slots &&
+    const bool xcd = !m->xcd_off && m->step_one_each && T <= m->max_slots &&
                      attention_xcd_merge(T, c.n_heads, c.n_kv_heads, hd, c.max_seq, true);
-    if (xcd) xq = attention_xcd_view(m->att_xcd, m->max_slots, c.n_kv_heads, c.max_seq);
+    if (xcd) {
+        xq = attention_xcd_view(m->att_xcd, m->max_slots, c.n_kv_heads, c.max_seq);
+        xq.misplaced = m->status + 1;   // pinned host word, cleared before the step
+        xq.rot = knobs().attn_xcd_rot;
+    }
     if ((rc = launch_attention_pairs(d_blk, m->n_dec, m->tok_pos, m->tok2seq, m->kv_base, T, c.n_heads, c.max_seq,
                                       m->att_pml, s, xcd ? &xq : nullptr, c.n_kv_heads))) return rc;
     const int tpad = row_pad(T);
@@ -707,6 +727,50 @@ bool prompt_mfma_pays(const slate_hip_llama* m, slate_hip_llama_session_t* const
     return flops >= 6.0 * bytes;
 }
 
+// Enqueue one step (replaying the batch size's graph for decode-only
+// steps when graphs are on), wait for it and fold in its profile.
+int run_step(slate_hip_llama* m, int n, int T, bool want, hipStream_t s) {
+    m->h_status[1] = 0;   // set by the decode attention on a misplaced workgroup
+    int rc;
+    // decode-only steps repeat the same launch sequence for a given batch
+    // size: replay it as a HIP graph (the descriptor copy in the graph reads
+    // the pinned staging, so the step's inputs are current)
+    if (m->graphs_on && !m->prof_on && T == n) {
+        hipGraphExec_t ge = nullptr;
+        for (const auto& g : m->graphs)
+            if (g.n == n && g.want == want) ge = g.exec;
+        if (!ge) {
+            rc = capture_step(m, n, T, want, s, &ge);
+            if (rc) return rc;
+            m->graphs.push_back({n, want, ge});
+        }
+        if (hipGraphLaunch(ge, s) != hipSuccess) {
+            set_error(-7, "llama_step: graph launch failed");
+            return -7;
+        }
+    } else {
+        rc = enqueue_step(m, n, T, want, s);
+        if (rc) {
+            m->prof_recs.clear();
+            m->prof_used = 0;
+            return rc;
+        }
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        set_error(-7, "llama_step: device execution failed");
+        return -7;
+    }
+    if (m->prof_on) {
+        if (m->h_status[1] != 0) {   // the step runs again: its timings are dropped
+            m->prof_recs.clear();
+            m->prof_used = 0;
+        } else {
+            prof_collect(m);
+        }
+    }
+    return 0;
+}
+
 int new_common(slate_hip_llama* m, const slate_hip_llama_config_t* cfg, int max_slots, int max_tokens) {
     if (!valid_cfg(cfg)) {
         set_error(-1, "engine: invalid config");
@@ -719,7 +783,8 @@ int new_common(slate_hip_llama* m, const slate_hip_llama_config_t* cfg, int max_
     m->cfg = *cfg;
     m->max_slots = max_slots;
     m->max_tokens = max_tokens;
-    reload_knobs();   // the plan switches in force for this engine's steps
+    m->knobs = read_knobs();   // the switches in force for this engine's steps
+    KnobScope ks(&m->knobs);
     return alloc_runtime(m);
 }
 
@@ -970,6 +1035,7 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
     if (!m || !sessions || !n_new || !tokens || n < 1 || n > m->max_slots) return -1;
     const auto& c = m->cfg;
     std::lock_guard<std::mutex> lk(m->mu);
+    KnobScope ks(&m->knobs);
     int T = 0;
     for (int i = 0; i < n; ++i) {
         slate_hip_llama_session_t* s = sessions[i];
@@ -1028,36 +1094,22 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
     {
         std::lock_guard<std::mutex> lk2(g_enqueue_mu);
         const bool want = out_logits != nullptr;
-        int rc;
-        // decode-only steps repeat the same launch sequence for a given batch
-        // size: replay it as a HIP graph (the descriptor copy in the graph
-        // reads the pinned staging, so the step's inputs are current)
-        if (m->graphs_on && !m->prof_on && T == n) {
-            hipGraphExec_t ge = nullptr;
-            for (const auto& g : m->graphs)
-                if (g.n == n && g.want == want) ge = g.exec;
-            if (!ge) {
-                rc = capture_step(m, n, T, want, s, &ge);
-                if (rc) return rc;
-                m->graphs.push_back({n, want, ge});
-            }
-            if (hipGraphLaunch(ge, s) != hipSuccess) {
-                set_error(-7, "llama_step: graph launch failed");
-                return -7;
-            }
-        } else {
-            rc = enqueue_step(m, n, T, want, s);
-            if (rc) {
-                m->prof_recs.clear();
-                m->prof_used = 0;
-                return rc;
-            }
+        int rc = run_step(m, n, T, want, s);
+        if (rc) return rc;
+        if (m->h_status[1] != 0) {
+            // A workgroup of the decode attention ran on another XCD than the
+            // queue it took its unit from, so the in-kernel merge may have
+            // read partials another XCD's L2 still held: the step's results
+            // are not trusted.  Turn the in-kernel merge off for this engine
+            // and run the step again on the merge kernel.  Running it again
+            // is exact: a step recomputes everything from its tokens and the
+            // K/V rows before its positions, and rewrites the rows at its
+            // positions with the same values.
+            m->xcd_off = true;
+            for (const auto& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+            m->graphs.clear();
+            if ((rc = run_step(m, n, T, want, s))) return rc;
         }
-        if (hipStreamSynchronize(s) != hipSuccess) {
-            set_error(-7, "llama_step: device execution failed");
-            return -7;
-        }
-        if (m->prof_on) prof_collect(m);
     }
     if (m->h_status[0] != 0) {
         set_error(m->h_status[0], "llama_step: device packing rejected the descriptor (%d)", m->h_status[0]);
@@ -1083,9 +1135,21 @@ int slate_hip_llama_profile(slate_hip_llama_t* m, int enable) {
 
 int slate_hip_llama_kv_f16(const slate_hip_llama_t* m) { return m ? (m->kv_f16 ? 1 : 0) : -1; }
 
+int slate_hip_llama_attn_xcd_merge(const slate_hip_llama_t* m) {
+    if (!m) return -1;
+    const auto& c = m->cfg;
+    KnobScope ks(&m->knobs);
+    return !m->xcd_off && attention_xcd_merge(1, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq, true) ? 1 : 0;
+}
+
 int slate_hip_llama_graphs(slate_hip_llama_t* m, int enable) {
     if (!m) return -1;
     std::lock_guard<std::mutex> lk(m->mu);
+    if (enable && tracer_attached()) {
+        m->graphs_on = false;
+        set_error(-5, "llama_graphs: refused while a rocprofiler tool is attached; steps launch eagerly");
+        return -5;
+    }
     m->graphs_on = enable != 0;
     return 0;
 }

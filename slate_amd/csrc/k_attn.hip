@@ -1003,6 +1003,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_xcd_kernel(
     constexpr int NB = G * HD / 256;                   // operand blocks of a kv head's G heads
     __shared__ int s_last;
     const int xcc = blockIdx.x & 7, u = blockIdx.x >> 3;
+    if (threadIdx.x == 0 && xq.misplaced) {
+        // the merge below is only sound if this workgroup shares the L2 of
+        // every unit of its queue: report any other placement to the host,
+        // which then runs the step again without the in-kernel merge
+        uint32_t hw;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(hw));
+        if ((int)(hw & 15) != ((int)blockIdx.x + xq.rot) % 8) *(volatile int32_t*)xq.misplaced = 1;
+    }
     if (u >= xq.len[xcc]) return;                      // workgroup-uniform
     const int4 d = xq.units[(size_t)xcc * xq.cap + u];
     AttnUnit un;

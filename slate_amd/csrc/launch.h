@@ -78,6 +78,8 @@ struct AttnXcd {
     int cap;
     int max_tok;
     int max_tok_step;   // tokens of the step being launched (<= max_tok)
+    int32_t* misplaced; // set to 1 by a workgroup not on the XCD its queue assumes (nullptr: unchecked)
+    int rot;            // the check expects workgroup i on XCD (i + rot) % 8 (0 but in tests)
 };
 size_t attention_xcd_ints(int max_tok, int Hkv, int max_pos);
 AttnXcd attention_xcd_view(int32_t* base, int max_tok, int Hkv, int max_pos);

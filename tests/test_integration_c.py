@@ -6,7 +6,11 @@
 * the loader binding slate_amd/bind/slate_llama_to_hip.c, whose text is the
   C block of the integration guide's LLaMA section, compiles against slate's
   llama.h with its struct-layout asserts, and the built binding library
-  exports it.
+  exports it;
+* the default chooser slate_amd/bind/backend_default_hip.c, whose text is
+  the first C block of the guide's vtable section, compiles against slate's
+  backend.h, picks the compat vtable (never the device-pointer one) and is
+  the chooser the harness library exports.
 """
 import os
 import re
@@ -18,6 +22,7 @@ from tests.conftest import ROOT
 
 REF_INCLUDE = "/root/reference/include"
 BIND = os.path.join(ROOT, "slate_amd", "bind", "slate_llama_to_hip.c")
+CHOOSER = os.path.join(ROOT, "slate_amd", "bind", "backend_default_hip.c")
 
 pytestmark = pytest.mark.skipif(not os.path.isdir(REF_INCLUDE), reason="slate's headers are not mounted here")
 
@@ -78,6 +83,29 @@ def test_integration_binding_is_the_shipped_file_and_compiles(tmp_path):
     r = subprocess.run(["gcc", "-std=c11", "-c", "-I", REF_INCLUDE, "-I", str(inc), str(f), "-o",
                         str(tmp_path / "b.o")], capture_output=True, text=True)
     assert r.returncode != 0 and "theta_base" in r.stderr
+
+
+def test_integration_chooser_is_the_shipped_file_and_compiles(tmp_path):
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    sec = doc[doc.index("## 1. The backend vtables"):doc.index("## 2.")]
+    blocks = re.findall(r"```c\n(.*?)```", sec, flags=re.S)
+    assert blocks and blocks[0] == open(CHOOSER).read()
+    code = blocks[0]
+    # slate's callers of the default hand it host pointers: the chooser must
+    # return the compat vtable, and no line of it may call the device one
+    assert "slate_backend_hip_compat()" in code
+    assert not re.search(r"slate_backend_hip\s*\(", code)
+    rc, err = compile_c(tmp_path, code)
+    assert rc == 0, err
+
+
+def test_default_harness_library_exports_the_chooser():
+    so = os.path.join(ROOT, "oracle", "_ref", "libslate_default_hip.so")
+    if not os.path.exists(so):
+        pytest.skip("oracle/_ref not built")
+    out = subprocess.run(["nm", "-D", so], capture_output=True, text=True, check=True).stdout
+    assert re.search(r" T slate_backend_default$", out, flags=re.M)
+    assert re.search(r" U slate_backend_hip_compat$", out, flags=re.M)
 
 
 def test_binding_library_exports_the_binding():

@@ -29,6 +29,41 @@ def run_both(hip, f, raw, X, M, K):
     return Y0.to_array(np.float32, (B, M)), Y1.to_array(np.float32, (B, M))
 
 
+def device_free_bytes():
+    """Free device memory (hipMemGetInfo), after the backend stream drains."""
+    import ctypes
+    slate_amd.load_library().slate_hip_sync()
+    hip_rt = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip_rt.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_matmul_allocates_nothing(hip):
+    """Device free memory is the same before and after a noalloc call of the
+    largest kind (prompt kernel, 64 rows, ~30 MiB of operand and partials),
+    made before any other matmul of this module.  Decisive in a fresh
+    process (the module run alone), where the backend's own scratch holds
+    nothing the call could have reused."""
+    f = noalloc_fn()
+    rng = np.random.default_rng(30)
+    M, K, B = 28672, 4096, 64
+    raw = np.frombuffer(quantize_q4k(rng.normal(0, 0.02, (M, K)).astype(np.float32)), np.uint8).copy()
+    X = rng.normal(0, 1, (B, K)).astype(np.float32)
+    W = slate_amd.DeviceBuffer.from_array(raw)
+    Xd = slate_amd.DeviceBuffer.from_array(X)
+    Y = slate_amd.DeviceBuffer(B * M * 4)
+    before = device_free_bytes()
+    slate_amd.check(f(Y.p, W.p, Xd.p, B, M, K), "matmul_q4k_noalloc")
+    after = device_free_bytes()
+    assert after == before, (before, after)
+    hip.sync()
+    want = slate_amd.DeviceBuffer(B * M * 4)
+    slate_amd.check(hip.matmul_q4k(want.p, W.p, Xd.p, B, M, K), "matmul_q4k")
+    hip.sync()
+    assert relerr(Y.to_array(np.float32, (B, M)), want.to_array(np.float32, (B, M))) < 1e-6
+
+
 def test_noalloc_matmul_matches_the_allocating_entry(hip, orc):
     f = noalloc_fn()
     rng = np.random.default_rng(31)
