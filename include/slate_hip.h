@@ -305,13 +305,13 @@ int   slate_hip_llama_graphs(slate_hip_llama_t* m, int enable);
  * tolerance.  slate_hip_llama_session_kv returns f32 either way. */
 int   slate_hip_llama_kv_f16(const slate_hip_llama_t* m);
 /* 1 while the engine's decode steps merge the attention chunks inside the
- * decode attention kernel (workgroup i takes its work from a queue of XCD
- * i % 8 and the merging unit reads the partials from that XCD's L2), 0 when
- * they use the separate merge kernel: shapes the in-kernel merge does not
- * take, SLATE_HIP_ATTN_XCD=0, a device where the placement probe failed, or
- * after a launch reported a workgroup on another XCD (the engine then runs
- * that step again on the merge kernel and keeps to it).  No slate
- * counterpart. */
+ * decode attention kernel (workgroup i takes its work from queue i % 8, the
+ * workgroups of a queue share one XCD, and the merging unit reads the
+ * partials from that XCD's L2), 0 when they use the separate merge kernel:
+ * shapes the in-kernel merge does not take, SLATE_HIP_ATTN_XCD=0, a device
+ * where the placement probe failed, or after a merge found a partial
+ * written on another XCD (the engine then runs that step again on the merge
+ * kernel and keeps to it).  No slate counterpart. */
 int   slate_hip_llama_attn_xcd_merge(const slate_hip_llama_t* m);
 int   slate_hip_llama_profile_read(slate_hip_llama_t* m, int cls, double* ms, double* bytes,
                                    int64_t* launches);

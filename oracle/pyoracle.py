@@ -318,3 +318,12 @@ class RefSession:
 
     def set_state(self, K, V, pos):
         return self.m.ref.lib.ref_session_set_state(self.h, fp(K), fp(V), pos)
+
+    def kv(self):
+        """The session's K/V caches, [n_layers, max_seq, kv_dim] each."""
+        c = self.m.cfg
+        shp = (c.n_layers, c.max_seq, c.n_kv_heads * c.head_dim)
+        K = np.empty(shp, np.float32)
+        V = np.empty(shp, np.float32)
+        assert self.m.ref.lib.ref_session_get_kv(self.h, fp(K), fp(V)) == 0
+        return K, V

@@ -335,6 +335,13 @@ class Llama:
         check(0 if r == n else r, f"get_tensor({name})")
         return buf, dt.value
 
+    def tensor_dtype(self, name):
+        """slate dtype of a weight (no copy)."""
+        dt = C.c_int(0)
+        if self.lib.slate_hip_llama_get_tensor(self.h, name.encode(), None, 0, C.byref(dt)) < 0:
+            raise KeyError(name)
+        return dt.value
+
     def session(self):
         return Session(self)
 

@@ -119,7 +119,7 @@ Knobs read_knobs() {
     k.attn_rope = env_int("SLATE_HIP_ATTN_ROPE", 1);
     if (k.attn_rope != 0 && k.attn_rope != 2) k.attn_rope = 1;
     k.attn_xcd = env_int("SLATE_HIP_ATTN_XCD", 1) != 0;
-    k.attn_xcd_rot = env_int("SLATE_HIP_ATTN_XCD_ROT", 0) & 7;
+    k.attn_xcd_tamper = env_int("SLATE_HIP_ATTN_XCD_TAMPER", 0) != 0;
     k.attn_mfma = std::min(2, std::max(0, env_int("SLATE_HIP_ATTN_MFMA", 1)));
     k.q4k_w = env_int("SLATE_HIP_Q4K_W", 8) == 4 ? 4 : 8;
     k.q4k_r = env_int("SLATE_HIP_Q4K_R", 0);

@@ -59,9 +59,9 @@ struct Knobs {
     int attn_wave = 1;     // SLATE_HIP_ATTN_WAVE=0: phased decode attention for every shape
     int attn_rope = 1;     // SLATE_HIP_ATTN_ROPE: 0 RoPE/append in their own kernel, 2 fused into the phased kernel
     int attn_xcd = 1;      // SLATE_HIP_ATTN_XCD=0: decode attention partials merged by their own kernel
-    int attn_xcd_rot = 0;  // SLATE_HIP_ATTN_XCD_ROT=r (tests): the placement check of the in-kernel merge
-                           // expects workgroup i on XCD (i + r) % 8, so r != 0 makes every launch report a
-                           // misplacement and exercises the engine's fallback
+    int attn_xcd_tamper = 0;  // SLATE_HIP_ATTN_XCD_TAMPER=1 (tests): the in-kernel merge's placement check
+                              // expects tags no unit writes, so every merge reports a partial from another
+                              // XCD and the engine's fallback runs
     int attn_mfma = 1;     // SLATE_HIP_ATTN_MFMA: prompt blocks on the MFMA kernel 0 never, 1 when the
                            // step's prompt work outweighs its decode work, 2 whenever a step has prompt chunks
     int q4k_w = 8;         // SLATE_HIP_Q4K_W: waves per decode workgroup (4 or 8)

@@ -217,6 +217,10 @@ int alloc_runtime(slate_hip_llama* m) {
     // decode steps (one token per sequence, at most max_slots rows) merge
     // the attention chunks inside the attention kernel from per-XCD queues
     if (dalloc(m, &m->att_xcd, attention_xcd_ints(m->max_slots, c.n_kv_heads, c.max_seq))) return -2;
+    if (hipMemset(m->att_xcd, 0, attention_xcd_ints(m->max_slots, c.n_kv_heads, c.max_seq) * 4) != hipSuccess) {
+        set_error(-7, "engine: attention queue clear failed");
+        return -7;
+    }
     attention_xcd_probe();
     // Q4_K activation operand for the widest matmul input (max(D, H)), T_pad rows
     const int Kmax = std::max(D, H);
@@ -554,7 +558,8 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
     if (xcd) {
         xq = attention_xcd_view(m->att_xcd, m->max_slots, c.n_kv_heads, c.max_seq);
         xq.misplaced = m->status + 1;   // pinned host word, cleared before the step
-        xq.rot = knobs().attn_xcd_rot;
+        xq.layer = 0;
+        xq.rot = knobs().attn_xcd_tamper ? 7 : 0;
     }
     if ((rc = launch_attention_pairs(d_blk, m->n_dec, m->tok_pos, m->tok2seq, m->kv_base, T, c.n_heads, c.max_seq,
                                       m->att_pml, s, xcd ? &xq : nullptr, c.n_kv_heads))) return rc;
@@ -594,11 +599,13 @@ int enqueue_step(slate_hip_llama* m, int n, int T, bool want_logits, hipStream_t
             // one token per sequence: RoPE and the K/V append run inside the
             // attention kernel; otherwise (prompt chunks) before it
             rc = 1;
+            AttnXcd xl = xq;
+            xl.layer = li;
             if (m->step_one_each)
                 rc = launch_attention_rope(m->att, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
                                            m->rope_cs, rn, m->tok_pos, T, c.n_heads, c.n_kv_heads, hd,
                                            m->head_stride, c.max_seq, m->att_po, m->att_pml, gi.q4 ? &a : nullptr, s,
-                                           prof_ev(m, ea), prof_ev(m, eb), m->kv_f16, xcd ? &xq : nullptr);
+                                           prof_ev(m, ea), prof_ev(m, eb), m->kv_f16, xcd ? &xl : nullptr);
             if (rc < 0) return rc;
             if (rc > 0) {
                 if ((rc = launch_rope_kv(m->q, Kl, Vl, m->part, S, (int64_t)tpad * (D + 2 * kvd), D + 2 * kvd,
@@ -1097,10 +1104,9 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
         int rc = run_step(m, n, T, want, s);
         if (rc) return rc;
         if (m->h_status[1] != 0) {
-            // A workgroup of the decode attention ran on another XCD than the
-            // queue it took its unit from, so the in-kernel merge may have
-            // read partials another XCD's L2 still held: the step's results
-            // are not trusted.  Turn the in-kernel merge off for this engine
+            // A merge inside the decode attention found a partial of its pair
+            // written on another XCD, so it may have read what that XCD's L2
+            // still held: the step's results are not trusted.  Turn the in-kernel merge off for this engine
             // and run the step again on the merge kernel.  Running it again
             // is exact: a step recomputes everything from its tokens and the
             // K/V rows before its positions, and rewrites the rows at its

@@ -238,6 +238,7 @@ __global__ __launch_bounds__(1024) void attn_pairs_kernel(const int32_t* __restr
     }
     if (tid == 0) pairs[0] = s_base;
     if (xq.len && tid < 8) xq.len[tid] = (Hkv >> 3) * s_base;
+    if (xq.len && tid == 0) xq.stepc[0] = xq.stepc[0] + 1;   // a new sequence of launch tags
 }
 
 // Unit u of the list (both loads issued before either is used; u may lie
@@ -853,14 +854,25 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
 // ---------------------------------------------------------------------------
 // Decode attention with the chunk merge inside (steps in which every
 // sequence adds one token).  Workgroups are dealt to the eight XCDs in turn
-// (workgroup i to XCD i % 8) and each XCD has its own L2; the workgroups of
-// XCD x take their units from queue x, which holds every chunk of the
-// (token, kv head) pairs assigned to it.  The unit that
-// finishes a pair's last chunk (an atomic count per pair) merges the pair's
-// G heads: its partials were written by units of the same XCD, whose stores
-// completed in that L2 before they counted (a wait for the stores, a
-// barrier, then the count), and it reads them with loads that miss in L1.
-// No writeback of L2 to memory is needed, as it would be across XCDs.
+// and each XCD has its own L2; workgroup i takes its unit from queue i % 8,
+// which holds every chunk of the (token, kv head) pairs assigned to it, so
+// all of a pair's units run on one XCD as long as the workgroups i with the
+// same i % 8 do (a launch whose first workgroup goes to XCD s, with the
+// rest following in turn, keeps that).  The unit that finishes a pair's last
+// chunk (an atomic count per pair) merges the pair's G heads: its partials
+// were written by units of the same XCD, whose stores completed in that L2
+// before they counted (a wait for the stores, a barrier, then the count),
+// and it reads them with loads that miss in L1.  No writeback of L2 to
+// memory is needed, as it would be across XCDs.
+//
+// Each launch checks that assumption itself: every unit writes a tag beside
+// its partial -- the launch's sequence number (the step count the queue
+// builder keeps, and the layer) and the XCD it ran on -- and the merging
+// unit compares every tag of its pair with its own.  A partial written on
+// another XCD cannot show this launch's tag with the merger's XCD (its tag
+// is either not visible from this L2 or names the other XCD), so any merge
+// that read across XCDs is reported to the host, which runs the step again
+// on the separate merge kernel.
 
 __global__ void xcc_probe_kernel(int32_t* out) {
     uint32_t x;
@@ -870,9 +882,11 @@ __global__ void xcc_probe_kernel(int32_t* out) {
 
 static int device_cus();
 
-// Whether workgroup i of a launch runs on XCD i % 8 of an eight-XCD device
-// (read from the hardware register by 64 workgroups), once per device and
-// process; -1: not probed yet.
+// Whether consecutive workgroups of a launch run on consecutive XCDs of an
+// eight-XCD device (workgroup i on XCD (i + s) % 8 for the launch's first
+// XCD s; measured on MI355X: s = 0 on the null stream, s = 7 on the backend
+// stream, the same for every launch), read from the hardware register by 64
+// workgroups, once per device and process; -1: not probed yet.
 constexpr int XCD_MAX_DEVICES = 64;
 static std::atomic<int> g_xcd_rr[XCD_MAX_DEVICES];
 static std::once_flag g_xcd_init;
@@ -898,28 +912,35 @@ bool attention_xcd_probe() {
         ok = hipGetLastError() == hipSuccess && hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess;
         (void)hipFree(d);
     }
-    for (int i = 0; ok && i < 64; ++i) ok = (h[i] & 15) == i % 8;
+    for (int i = 0; ok && i < 64; ++i) ok = (h[i] & 8) == 0 && ((h[i] - h[0]) & 7) == i % 8;
     f->store(ok ? 1 : 0);
     return ok;
+}
+
+static size_t xcd_fixed_ints(int max_tok, int Hkv, size_t nch) {
+    return (12 + (size_t)max_tok * Hkv * (1 + nch) + 3) / 4 * 4;
 }
 
 size_t attention_xcd_ints(int max_tok, int Hkv, int max_pos) {
     const size_t nch = (size_t)(max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t cap = ((size_t)max_tok * Hkv + 7) / 8 * nch;
-    const size_t fixed = (8 + (size_t)max_tok * Hkv + 3) / 4 * 4;
-    return fixed + 8 * cap * 4;
+    return xcd_fixed_ints(max_tok, Hkv, nch) + 8 * cap * 4;
 }
 
 // Layout of attention_xcd_ints(max_tok, Hkv, max_pos) int32s from a
-// 16-byte aligned base: len, arrive, then the eight queues.
+// 16-byte aligned base: len [8], the step count [1] (+3 padding), arrive,
+// tags, then the eight queues.
 AttnXcd attention_xcd_view(int32_t* base, int max_tok, int Hkv, int max_pos) {
-    const size_t fixed = (8 + (size_t)max_tok * Hkv + 3) / 4 * 4;
+    const size_t nch = (size_t)(max_pos + ATT_CHUNK - 1) / ATT_CHUNK;
     AttnXcd x{};
     x.len = base;
-    x.arrive = x.len + 8;
-    x.units = (int4*)(base + fixed);
+    x.stepc = base + 8;
+    x.arrive = base + 12;
+    x.tag = x.arrive + (size_t)max_tok * Hkv;
+    x.units = (int4*)(base + xcd_fixed_ints(max_tok, Hkv, nch));
     x.max_tok = max_tok;
-    x.cap = (int)(((size_t)max_tok * Hkv + 7) / 8 * ((max_pos + ATT_CHUNK - 1) / ATT_CHUNK));
+    x.nch = (int)nch;
+    x.cap = (int)(((size_t)max_tok * Hkv + 7) / 8 * nch);
     return x;
 }
 
@@ -989,12 +1010,13 @@ __global__ __launch_bounds__(1024) void attn_xcd_queues_kernel(const int32_t* __
         __syncthreads();
     }
     if (tid < 8) xq.len[tid] = s_base[tid];
+    if (tid == 0) xq.stepc[0] = xq.stepc[0] + 1;   // a new sequence of launch tags
 }
 
-// One unit per workgroup: workgroup i runs on XCD i % 8 (the dispatch order,
-// checked once per process by attention_xcd_probe) and takes unit i / 8 of
-// that XCD's queue; the grid covers the longest queue and the surplus
-// workgroups exit.
+// One unit per workgroup: workgroup i takes unit i / 8 of queue i % 8 (the
+// workgroups of one queue share an XCD, as the dispatch order gives and the
+// tags check); the grid covers the longest queue and the surplus workgroups
+// exit.
 template <int HD, int G, typename KVT>
 __global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_xcd_kernel(
     const KVT* Kp, const KVT* Vp, int Hq, int Hkv, int64_t head_stride, int nch_max, float* __restrict__ po,
@@ -1003,14 +1025,6 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_xcd_kernel(
     constexpr int NB = G * HD / 256;                   // operand blocks of a kv head's G heads
     __shared__ int s_last;
     const int xcc = blockIdx.x & 7, u = blockIdx.x >> 3;
-    if (threadIdx.x == 0 && xq.misplaced) {
-        // the merge below is only sound if this workgroup shares the L2 of
-        // every unit of its queue: report any other placement to the host,
-        // which then runs the step again without the in-kernel merge
-        uint32_t hw;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(hw));
-        if ((int)(hw & 15) != ((int)blockIdx.x + xq.rot) % 8) *(volatile int32_t*)xq.misplaced = 1;
-    }
     if (u >= xq.len[xcc]) return;                      // workgroup-uniform
     const int4 d = xq.units[(size_t)xcc * xq.cap + u];
     AttnUnit un;
@@ -1021,15 +1035,31 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_xcd_kernel(
     un.kvb = (int64_t)(((uint64_t)((uint32_t)d.w & 0xffffffu) << 32) | (uint64_t)(uint32_t)d.z);
     const int h = (int)((uint32_t)d.w >> 24);
     attn_dec_wave_unit<HD, G, KVT, true>(nullptr, Kp, Vp, un, h, Hq, head_stride, nch_max, po, pml, fr, Hkv);
-    SH_WAIT_VMCNT(0);                                  // this thread's partial stores are in L2
+    uint32_t hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(hw));
+    const uint32_t mytag = ((uint32_t)xq.stepc[0] * 4096u + (uint32_t)xq.layer) * 16u + (hw & 15u);
+    const int pair = un.t * Hkv + h;
+    if (threadIdx.x == 0) xq.tag[(size_t)pair * xq.nch + un.c] = (int32_t)mytag;
+    SH_WAIT_VMCNT(0);                                  // this thread's partial (and tag) stores are in L2
     __syncthreads();
     const int nch = min((un.p + ATT_CHUNK) / ATT_CHUNK, nch_max);
     if (threadIdx.x == 0) {
-        s_last = atomicAdd(&xq.arrive[un.t * Hkv + h], 1) == nch - 1;
-        if (s_last) atomicExch(&xq.arrive[un.t * Hkv + h], 0);   // every chunk has counted: ready for the next layer
+        s_last = atomicAdd(&xq.arrive[pair], 1) == nch - 1;
+        if (s_last) atomicExch(&xq.arrive[pair], 0);   // every chunk has counted: ready for the next layer
     }
     __syncthreads();
     if (!s_last) return;
+    if (xq.misplaced) {
+        // every chunk of the pair written in this launch on this XCD?
+        const __amdgpu_buffer_rsrc_t tr = __builtin_amdgcn_make_buffer_rsrc(
+            xq.tag, 0, (int)((size_t)xq.max_tok * Hkv * xq.nch * 4), 0x00020000);
+        const uint32_t want = mytag ^ ((uint32_t)xq.rot << 28);
+        for (int c = threadIdx.x; c < nch; c += ATT_THREADS) {
+            const uint32_t got = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                tr, (int)(((size_t)pair * xq.nch + c) * 4), 0, 1);
+            if (got != want) *(volatile int32_t*)xq.misplaced = 1;
+        }
+    }
     const PartL2 pp{__builtin_amdgcn_make_buffer_rsrc(po, 0, (int)po_bytes, 0x00020000),
                     __builtin_amdgcn_make_buffer_rsrc(pml, 0, (int)pml_bytes, 0x00020000)};
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -1264,7 +1294,7 @@ static int device_cus() {
 
 bool attention_xcd_merge(int T, int Hq, int Hkv, int HD, int max_pos, bool has_act) {
     (void)has_act;
-    // workgroup i on XCD i % 8, as probed (attention_xcd_probe) for this device
+    // consecutive workgroups on consecutive XCDs, as probed (attention_xcd_probe) for this device
     if (!knobs().attn_xcd || rope_fused() != 1 || !wave_kernel() || T <= 0 || T > ATT_WAVE_MAX_TOKENS ||
         Hkv <= 0 || Hq % Hkv != 0)
         return false;

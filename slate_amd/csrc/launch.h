@@ -73,18 +73,25 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
 // from its own XCD's L2 inside the attention kernel.
 struct AttnXcd {
     int32_t* len;       // [8] units per queue
+    int32_t* stepc;     // [1] steps counted by the queue builders (the launch tags' sequence)
     int32_t* arrive;    // [max_tok * Hkv] finished chunks per (token, kv head)
+    int32_t* tag;       // [max_tok * Hkv][nch] the launch and XCD that wrote each chunk's partial
     int4* units;        // [8][cap] {t * 65536 + c, p, kv base low, kv base high | h << 24}
     int cap;
     int max_tok;
+    int nch;            // key chunks per pair the tags are laid out for
     int max_tok_step;   // tokens of the step being launched (<= max_tok)
-    int32_t* misplaced; // set to 1 by a workgroup not on the XCD its queue assumes (nullptr: unchecked)
-    int rot;            // the check expects workgroup i on XCD (i + rot) % 8 (0 but in tests)
+    int layer;          // the launch's layer (part of its tags)
+    int32_t* misplaced; // set to 1 when a merge found a partial written on another XCD (nullptr: unchecked)
+    int rot;            // nonzero (tests only): the merge expects tags no unit writes, so every merge reports
 };
 size_t attention_xcd_ints(int max_tok, int Hkv, int max_pos);
 AttnXcd attention_xcd_view(int32_t* base, int max_tok, int Hkv, int max_pos);
-// Checks once per process (a 64-workgroup launch and a copy) that workgroup i
-// runs on XCD i % 8; attention_xcd_merge is false until it has returned true.
+// Checks once per process (a 64-workgroup launch and a copy) that
+// consecutive workgroups run on consecutive XCDs; attention_xcd_merge is
+// false until it has returned true.  Each launch also checks itself (the
+// tags), so the probe only keeps the kernel off a device where the placement
+// is not what it assumes at all.
 bool attention_xcd_probe();
 int launch_attention_rope(float* out, void* Kp, void* Vp, const float* part, int nsplit, int64_t split_stride,
                           int qkv_ld, const float* cs, const RowNorm& rn, const int32_t* tok_pos, int T, int Hq,

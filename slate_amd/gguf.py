@@ -40,7 +40,7 @@ class TensorEntry:
     name: str
     shape: tuple          # outermost-first, e.g. (out, in)
     ggml_type: int
-    data: bytes | np.ndarray
+    data: object          # bytes, or a callable returning an array or bytes
 
 
 @dataclass
@@ -59,11 +59,27 @@ class GGUFWriter:
         self.kv.append((key, T_STRING, str(v)))
 
     def add_tensor(self, name, shape, ggml_type, data):
+        """data: an array or bytes, or a callable returning one, called when
+        the file is written (so a large model streams through host memory one
+        tensor at a time)."""
         numel = int(np.prod(shape))
-        raw = data.tobytes() if isinstance(data, np.ndarray) else bytes(data)
-        if len(raw) != _nbytes(ggml_type, numel):
-            raise ValueError(f"{name}: {len(raw)} bytes, expected {_nbytes(ggml_type, numel)}")
+        if callable(data):
+            raw = data
+        else:
+            raw = data.tobytes() if isinstance(data, np.ndarray) else bytes(data)
+            if len(raw) != _nbytes(ggml_type, numel):
+                raise ValueError(f"{name}: {len(raw)} bytes, expected {_nbytes(ggml_type, numel)}")
         self.tensors.append(TensorEntry(name, tuple(int(s) for s in shape), ggml_type, raw))
+
+    @staticmethod
+    def _payload(te):
+        """The tensor's bytes (fetched now for a lazy tensor), size-checked."""
+        data = te.data() if callable(te.data) else te.data
+        mv = memoryview(np.ascontiguousarray(data) if isinstance(data, np.ndarray) else data).cast("B")
+        want = _nbytes(te.ggml_type, int(np.prod(te.shape)))
+        if mv.nbytes != want:
+            raise ValueError(f"{te.name}: {mv.nbytes} bytes, expected {want}")
+        return mv
 
     @staticmethod
     def _str(s: str) -> bytes:
@@ -86,7 +102,7 @@ class GGUFWriter:
         for te in self.tensors:
             off = (off + self.alignment - 1) // self.alignment * self.alignment
             offsets.append(off)
-            off += len(te.data)
+            off += _nbytes(te.ggml_type, int(np.prod(te.shape)))
         for te, o in zip(self.tensors, offsets):
             hdr += self._str(te.name) + struct.pack("<I", len(te.shape))
             for d in reversed(te.shape):          # innermost first
@@ -99,8 +115,10 @@ class GGUFWriter:
             pos = 0
             for te, o in zip(self.tensors, offsets):
                 f.write(b"\0" * (o - pos))
-                f.write(te.data)
-                pos = o + len(te.data)
+                mv = self._payload(te)
+                f.write(mv)
+                pos = o + mv.nbytes
+                del mv
 
 
 class GGUFFile:

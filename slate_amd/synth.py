@@ -193,14 +193,24 @@ def write_llama_gguf(path, shape: LlamaShape, tensors: dict):
     g.write(path)
 
 
-def engine_tensors(m, shape: LlamaShape) -> dict:
+def engine_tensors(m, shape: LlamaShape, lazy: bool = False) -> dict:
     """The weights of a device engine (slate_amd.Llama) copied back to the
     host in make_llama's form {name: (array, slate dtype, (out, in) shape)},
     Q4_K and Q8_0 in slate's row layout, ready for write_llama_gguf or the
-    oracle."""
+    oracle.  lazy=True: each array is a callable that copies the tensor when
+    called (write_llama_gguf then holds one tensor at a time)."""
     t = {}
 
+    def fetch(name, dt):
+        raw, got = m.get_tensor(name)
+        assert got == dt
+        return raw.view(np.float32) if dt == SLATE_F32 else raw
+
     def get(name, key, shp):
+        if lazy:
+            dt = m.tensor_dtype(name)
+            t[key] = ((lambda n=name, d=dt: fetch(n, d)), dt, shp)
+            return
         raw, dt = m.get_tensor(name)
         t[key] = (raw.view(np.float32) if dt == SLATE_F32 else raw, dt, shp)
 

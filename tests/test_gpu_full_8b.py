@@ -15,7 +15,10 @@ reference feeds the GPU's first greedy token into its second step, so the
 second step also compares the reference's own K/V append with the GPU's.
 A third, mixed step (the decode tokens beside a new sequence's 300-token
 prompt, all rows on the prompt kernels) is checked the same way, and the new
-sequence's logits against its prompt prefilled alone (1e-4).  One sequence
+sequence's logits against its prompt prefilled alone (1e-4).  Then every
+sequence takes a 32-token prompt chunk in one step, against slate's
+token-serial prefill of the same tokens from the reference's own state: the
+K/V rows written in every layer (1e-4) and the last logits (1e-3).  One sequence
 prefilled and decoded alone gets the logits it gets in the batch (within
 1e-4), and the whole run repeated in fresh sessions gets the same bits."""
 import os
@@ -146,6 +149,29 @@ def test_8b_full_size_decode_matches_reference():
         assert rc == 0 and relerr(lg3[NSEQ], la) < 1e-4
         alone.free()
         new.free()
+        # prompt chunks at the full shape: a 32-token chunk at every
+        # sequence's position (contexts ~130-2050) in one step of 512 rows
+        # (the MFMA prompt GEMM, RoPE + K/V append of prompt rows, the MFMA
+        # prompt attention) against slate's prefill of the same tokens, 32
+        # token-serial decode steps (llama_infer.c:262-272) from the
+        # reference's own state: the 32 K/V rows written in every layer
+        # (rel 1e-4 per layer) and each sequence's last logits (rel 1e-3)
+        chunk = rng.integers(0, SHAPE.vocab, (NSEQ, 32)).astype(np.int32)
+        p0 = [s.position for s in sess]
+        rc, lg4, nx4 = m.step(sess, [32] * NSEQ, chunk.reshape(-1))
+        assert rc == 0 and np.all(np.isfinite(lg4))
+        for k in range(32):
+            want = ref.decode(chunk[:, k])
+        for i in range(NSEQ):
+            assert relerr(lg4[i], want[i]) < TOL, (i, relerr(lg4[i], want[i]))
+            assert int(nx4[i]) == int(np.argmax(want[i])) or not gap_ok(want[i]), i
+            K, V = sess[i].kv()
+            Kr, Vr = ref.rs[i].kv()
+            rows = slice(p0[i], p0[i] + 32)
+            for li in range(SHAPE.n_layers):
+                ek, ev = relerr(K[li, rows], Kr[li, rows]), relerr(V[li, rows], Vr[li, rows])
+                assert ek < 1e-4 and ev < 1e-4, (i, li, ek, ev)
+            del K, V, Kr, Vr
     finally:
         ref.close()
     # batch invariance: the first sequence alone
