@@ -51,6 +51,13 @@ clip(round(exp(N(ln 1024, 1))), 16, 16384).  Each figure is the device time
 of a captured graph of many calls (no host launch gaps) divided by the calls.
 --copy-calibration instead runs a plain device copy of known size (for
 scaling the PMC byte counters).
+
+--summarize DIR writes the summaries in profiles/ from the rocprofv3 output
+of the runs each summary names at its top (run with -d DIR/<name>), with no
+GPU: kernel-trace breakdowns per step (steps split at each
+pack_batch_kernel), per-shape Q4_K decode matmul figures, and the PMC
+traffic table whose per-launch figure the bench line reports as
+roofline.traffic.
 """
 import argparse
 import json
@@ -272,6 +279,8 @@ def run_c4(args, shape):
                    "prompt_tokens": prompt_tokens,
                    "mean_context_start": round(float(np.mean(ctx0)), 1)},
         "decode_only_tok_s": None if dec_tok_s is None else round(dec_tok_s, 1),
+        "operands": "Q4_K weights dequantised exactly to f16 (q * scale) against f32 activations split into two "
+                    "f16 halves (hi + lo, ~22-bit significands), f32 accumulation; f32 K/V cache and attention",
         "roofline": roofline,
         "kernels": {"profiled_steps": args.profile_steps, "other_decode_class": other,
                     f"{other}_GBs": round(oby / max(oms, 1e-9) / 1e6, 1), f"{other}_ms": round(oms, 2),
@@ -306,7 +315,8 @@ class PoissonWorkload:
         self.prefill_chunk = prefill_chunk
         self.queue, self.active = [], []
         self.next_arrival = float(self.rng.exponential(1.0 / rate))
-        self.arrived = self.completed = self.generated = 0
+        self.arrived = self.completed = self.generated = self.prompt_tokens = 0
+        self.last_rows = self.last_seqs = 0
 
     def admit(self, now):
         while self.next_arrival <= now:
@@ -343,6 +353,8 @@ class PoissonWorkload:
                 toks.append(r["prompt"][r["done"]:r["done"] + c])
         rc, _, nxt = self.m.step([r["sess"] for r in rows], n_new, np.concatenate(toks), want_logits=False)
         assert rc == 0, f"step rc={rc}"
+        self.last_rows, self.last_seqs = int(sum(n_new)), len(rows)
+        self.prompt_tokens += sum(n for r, n in zip(rows, n_new) if r["done"] < len(r["prompt"]))
         gen = 0
         for r, n, t in zip(rows, n_new, nxt):
             if r["done"] < len(r["prompt"]):
@@ -375,7 +387,7 @@ def run_c5(args, shape):
         wl.step(now)
         now = time.perf_counter() - start
     lib.slate_hip_sync()
-    g0, a0, c0 = wl.generated, wl.arrived, wl.completed
+    g0, a0, c0, p0 = wl.generated, wl.arrived, wl.completed, wl.prompt_tokens
     steps, batch_sum, t_begin = 0, 0, time.perf_counter()
     while time.perf_counter() - t_begin < args.duration:
         now = time.perf_counter() - start
@@ -387,8 +399,25 @@ def run_c5(args, shape):
     lib.slate_hip_sync()
     dt = time.perf_counter() - t_begin
     tokens = wl.generated - g0
-    log(f"{steps} steps in {dt:.1f} s: {tokens} tokens, {wl.arrived - a0} arrivals, "
-        f"{wl.completed - c0} completed, mean batch {batch_sum / max(steps, 1):.1f}, queue {len(wl.queue)}")
+    prompt_tok = wl.prompt_tokens - p0
+    queued = len(wl.queue)
+    log(f"{steps} steps in {dt:.1f} s: {tokens} tokens, {prompt_tok} prompt tokens, {wl.arrived - a0} arrivals, "
+        f"{wl.completed - c0} completed, mean batch {batch_sum / max(steps, 1):.1f}, queue {queued}")
+    # the Q4_K matmuls of a few steps after the window, event-timed: useful
+    # flops 2 * rows * (linear weights of the layers) + 2 * sequences * (LM
+    # head weights) per step over their device time
+    D, H, kvd = shape.d_model, shape.ffn, shape.kv_dim
+    layer_w = shape.n_layers * (D * D * 2 + kvd * D * 2 + 3 * H * D)
+    flops = 0.0
+    m.profile(True)
+    for _ in range(args.profile_steps):
+        if wl.step(time.perf_counter() - start)[1]:
+            flops += 2.0 * (wl.last_rows * layer_w + wl.last_seqs * shape.vocab * D)
+    m.profile(False)
+    lib.slate_hip_sync()
+    raw = m.profile_read()
+    mm_ms = raw["q4k_mm"][0] + raw["q4k_mm_pf"][0]
+    tflops = flops / (mm_ms * 1e-3) / 1e12 if mm_ms > 0 else None
     return {
         "metric": "generated tok/s, 70B-shape Q4_K, Poisson 4 req/s, B<=32 (mixed prefill + decode)",
         "value": round(tokens / dt, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup_s": args.warmup_s,
@@ -401,7 +430,13 @@ def run_c5(args, shape):
                    "heads": f"{shape.n_heads}q/{shape.n_kv_heads}kv", "ffn": shape.ffn, "vocab": shape.vocab,
                    "weights": "q4_k", "max_batch": max_batch, "arrivals": wl.arrived - a0,
                    "completed": wl.completed - c0, "mean_batch": round(batch_sum / max(steps, 1), 2),
-                   "queued_at_end": len(wl.queue)},
+                   "queued_at_end": queued, "prompt_tok_s": round(prompt_tok / dt, 1)},
+        "operands": "Q4_K weights dequantised exactly to f16 (q * scale) against f32 activations split into two "
+                    "f16 halves (hi + lo, ~22-bit significands), f32 accumulation; f32 K/V and attention",
+        "prompt_matmul": {"profiled_steps": args.profile_steps, "device_ms": round(mm_ms, 2),
+                          "useful_TFLOPs": None if tflops is None else round(tflops, 1),
+                          "frac_f16_peak": None if tflops is None else round(tflops / 2500.0, 4),
+                          "note": "every Q4_K matmul launch of the profiled steps; two f16 MFMAs per product"},
     }
 
 
@@ -425,7 +460,11 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 1 GiB device-to-device copy 5 times and exit")
     ap.add_argument("--ops", action="store_true", help="op-level Q4_K / Q8_0 matmul and ragged attention figures")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="write the profiles/ summaries from the rocprofv3 output under DIR (no GPU needed)")
     args = ap.parse_args()
+    if args.summarize:
+        return summarize(args.summarize)
     if args.profile_steps < 1:
         ap.error("--profile-steps must be at least 1")
     if args.copy_calibration:
@@ -708,6 +747,324 @@ def cpu_model():
     except OSError:
         pass
     return None
+
+
+# ---------------------------------------------------------------------------
+# Profile summaries (--summarize DIR): the text files under profiles/ from
+# the rocprofv3 output of the runs listed at the top of each file.
+
+D8, H8, KV8, V8 = 4096, 14336, 1024, 128256
+DEC_SHAPES = ("QKV 6144x4096", "O 4096x4096", "gate+up 2x14336x4096", "down 4096x14336", "lm_head 128256x4096")
+PROFILE_CMDS = {
+    "trace": "rocprofv3 --kernel-trace --stats --output-format csv -d $PROF/trace -o run -- "
+             "python3 bench.py --steps 64 --warmup 4 --no-cpu",
+    "pmc_fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $PROF/pmc_fetch -o run -- "
+                 "python3 bench.py --steps 8 --warmup 2 --no-cpu",
+    "pmc_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $PROF/pmc_write -o run -- "
+                 "python3 bench.py --steps 8 --warmup 2 --no-cpu",
+    "cal_fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d $PROF/cal_fetch -o run -- "
+                 "python3 bench.py --copy-calibration",
+    "cal_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d $PROF/cal_write -o run -- "
+                 "python3 bench.py --copy-calibration",
+    "ops": "python3 bench.py --ops > $PROF/ops.json",
+    "ops_trace": "rocprofv3 --kernel-trace --stats --output-format csv -d $PROF/ops_trace -o run -- "
+                 "python3 bench.py --ops",
+    "trace70": "rocprofv3 --kernel-trace --stats --output-format csv -d $PROF/trace70 -o run -- "
+               "python3 bench.py --shape 70b --duration 15 --warmup-s 5 > $PROF/trace70.json",
+}
+
+
+def _q4(M, K):
+    return M * K // 256 * 144
+
+
+def dec_alg_bytes(name, T=16):
+    """Algorithmic bytes of one 16-row decode matmul launch of the 8B shape:
+    weights once, activations in and out once."""
+    D, H, V = D8, H8, V8
+    return {"QKV 6144x4096": _q4(6144, D) + 4 * T * D + 4 * T * 6144,
+            "O 4096x4096": _q4(D, D) + 4 * T * D + 4 * T * D,
+            "gate+up 2x14336x4096": 2 * _q4(H, D) + 4 * T * D + 4 * T * 2 * H,
+            "down 4096x14336": _q4(D, H) + 4 * T * H + 4 * T * D,
+            "lm_head 128256x4096": _q4(V, D) + 4 * T * D + 4 * T * V}[name]
+
+
+def _one(pattern):
+    import glob
+    got = glob.glob(pattern, recursive=True)
+    if not got:
+        raise FileNotFoundError(pattern)
+    return got[0]
+
+
+def _kname(name):
+    return name.replace("void ", "").replace("slate_hip::", "").split("(")[0]
+
+
+def _dur_us(r):
+    return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+
+def trace_steps(path):
+    """Kernel-trace rows of a bench run split into engine steps (each step
+    starts with its pack_batch_kernel; the last, possibly cut, is dropped)."""
+    import csv
+    rows = list(csv.DictReader(open(_one(path + "/**/*kernel_trace.csv"))))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    steps, cur = [], None
+    for r in rows:
+        if "pack_batch_kernel" in r["Kernel_Name"]:
+            cur = []
+            steps.append(cur)
+        if cur is not None:
+            cur.append(r)
+    return steps[:-1]
+
+
+def has_prompt(step):
+    return any("q4k_pf_kernel" in r["Kernel_Name"] for r in step)
+
+
+def dec_launches(step):
+    """(row, shape) of the decode matmul launches of a decode step: QKV, O,
+    gate+up, down per layer in that order, then the LM head."""
+    ks = [r for r in step if _kname(r["Kernel_Name"]).startswith("q4k_dec_kernel")]
+    return [(r, DEC_SHAPES[4] if i == len(ks) - 1 else DEC_SHAPES[i % 4]) for i, r in enumerate(ks)]
+
+
+def step_breakdown(steps, top=14):
+    import collections
+    n = len(steps)
+    agg = collections.defaultdict(lambda: [0.0, 0])
+    span = busy = 0.0
+    for s in steps:
+        span += (max(int(r["End_Timestamp"]) for r in s) - int(s[0]["Start_Timestamp"])) / 1e3
+        for r in s:
+            busy += _dur_us(r)
+            a = agg[_kname(r["Kernel_Name"])]
+            a[0] += _dur_us(r)
+            a[1] += 1
+    out = [f"per step: span {span / n:.1f} us, kernel busy {busy / n:.1f} us, "
+           f"dispatches {sum(v[1] for v in agg.values()) / n:.1f}",
+           "  us/step calls/step   us/call  kernel"]
+    for k, (d, c) in sorted(agg.items(), key=lambda kv: -kv[1][0])[:top]:
+        out.append(f"  {d / n:9.1f}   {c / n:8.1f}  {d / c:8.2f}  {k}")
+    return out, agg
+
+
+def stats_lines(path, top=12):
+    import csv
+    out = ["  calls     avg us   total ms      %  kernel"]
+    for r in list(csv.DictReader(open(_one(path + "/**/*kernel_stats.csv"))))[:top]:
+        out.append(f"  {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
+                   f"{float(r['TotalDurationNs']) / 1e6:10.2f} {float(r['Percentage']):6.2f}  {_kname(r['Name'])}")
+    return out
+
+
+def _header(title, keys, extra=()):
+    out = [f"# {title}\n", "Commands (from the repository root, TMPDIR=/tmp, PROF = an output directory):"]
+    out += ["  " + PROFILE_CMDS[k] for k in keys]
+    out += ["  python3 bench.py --summarize $PROF", ""]
+    return out + list(extra)
+
+
+def summary_decode(prof):
+    import collections
+    import statistics
+    steps = trace_steps(prof + "/trace")
+    dec = [s for s in steps if not has_prompt(s)][2:]
+    n = len(dec)
+    out = _header("Decode step kernels, 8B-shape Q4_K engine, B=16 ragged (MI355X, one GPU)", ["trace"], [
+        "Per-step figures: dispatches of the kernel trace split into engine steps at each pack_batch_kernel;",
+        "decode-only steps (no q4k_pf_kernel, i.e. no prompt chunk) after the first two; 'alg' = algorithmic",
+        "bytes (weights once, activations in and out once) of each launch.  Kernel durations under the tracer",
+        "include its per-dispatch overhead (about 1 us); spans include the host time between steps.\n",
+        f"decode-only steps analysed: {n} (of {len(steps)} steps in the run)"])
+    b, _ = step_breakdown(dec)
+    out += b
+    per = collections.defaultdict(list)
+    for s in dec:
+        for r, name in dec_launches(s):
+            per[name].append(_dur_us(r))
+    out += ["\nq4k_dec_kernel by shape (decode steps, T=16 rows):",
+            "shape                      avg us   alg MB  alg GB/s  of 8 TB/s"]
+    tot_t = tot_b = cnt = 0
+    for name in DEC_SHAPES:
+        v, a = per[name], dec_alg_bytes(name)
+        m = statistics.mean(v)
+        out.append(f"{name:26s} {m:7.2f} {a / 1e6:8.2f} {a / m / 1e3:9.1f} {a / m / 1e3 / HBM_PEAK_GBS:10.3f}")
+        tot_t += sum(v)
+        tot_b += a * len(v)
+        cnt += len(v)
+    out.append(f"all q4k_dec launches: {cnt / n:.0f}/step, avg {tot_t / cnt:.2f} us, avg alg bytes "
+               f"{tot_b / cnt / 1e6:.2f} MB, {tot_b / tot_t / 1e3:.1f} GB/s ({tot_b / tot_t / 1e3 / HBM_PEAK_GBS:.3f})")
+    out.append("\nrocprofv3 --stats over the whole run (includes the untimed context prefill):")
+    out += stats_lines(prof + "/trace")
+    return "decode_step_8b_b16_kernels.txt", out
+
+
+def summary_prefill(prof):
+    import re
+    log_text = open(prof + "/trace.log").read() if os.path.exists(prof + "/trace.log") else ""
+    m = re.search(r"prefilled (\d+) context tokens", log_text)
+    steps = trace_steps(prof + "/trace")
+    first_dec = next(i for i, s_ in enumerate(steps) if not has_prompt(s_))
+    pre = steps[:first_dec]
+    mixed = [s for s in steps[first_dec:] if has_prompt(s)]
+    out = _header("Prompt steps, 8B-shape Q4_K engine (MI355X, one GPU)", ["trace"], [
+        "(trace.log: the run's stderr, for the count of context tokens)\n",
+        "Part 1: the steps before the first decode-only step: the bench's untimed context prefill, 16",
+        "sequences x U[128,2048] tokens packed into steps of up to 4096 tokens.  q4k_pf_kernel: 2*T*M*K",
+        "algorithmic flops per launch (T tokens of the step); every product runs as two f16 MFMAs (activation",
+        "hi and lo halves).  attn_prompt_kernel: the prompt tokens' attention on MFMA.\n",
+        f"== {len(pre)} context-prefill steps"])
+    b, agg = step_breakdown(pre, 10)
+    out += b
+    pf = sum(d for k, (d, c) in agg.items() if k.startswith("q4k_pf_kernel"))
+    att = sum(d for k, (d, c) in agg.items() if k.startswith("attn_prompt_kernel") or k.startswith("attn_merge"))
+    if m:
+        tokens = int(m.group(1))
+        lin = 6144 * D8 + D8 * D8 + 2 * H8 * D8 + D8 * H8
+        flops = 2.0 * tokens * lin * 32
+        out.append(f"\n{tokens} context tokens.  q4k_pf_kernel over these steps: {pf / 1e3:.1f} ms for "
+                   f"{flops / 1e12:.1f} TFLOP of linear layers -> {flops / pf / 1e6:.0f} TFLOP/s useful "
+                   f"({flops / pf / 1e6 / 2500:.3f} of the 2.5 PFLOP/s f16 peak; {2 * flops / pf / 1e6 / 2500:.3f} "
+                   "counting both MFMAs of each product)")
+        out.append(f"prompt attention (attn_prompt_kernel + attn_merge_kernel): {att / len(pre) / 1e3:.2f} ms per "
+                   f"step ({att / 1e3 / tokens * 1e3:.1f} us per 1k prompt tokens)")
+    out.append(f"\nPart 2: the {len(mixed)} steps with a prompt inside the timed window (the decode tokens and an")
+    out.append("arrival's 64-512-token prompt); attention per step on the MFMA prompt kernel or, where the")
+    out.append("decode tokens' K/V streaming outweighs the prompt work, on the tokenwise decode kernels")
+    if mixed:
+        b, _ = step_breakdown(mixed, 10)
+        out += b
+    return "prefill_chunks_8b_kernels.txt", out
+
+
+def summary_traffic(prof):
+    import collections
+    import csv
+
+    def pmc(path):
+        return list(csv.DictReader(open(_one(path + "/**/*counter_collection.csv"))))
+
+    def copyk(rows):
+        return max(float(r["Counter_Value"]) for r in rows
+                   if "copy" in r["Kernel_Name"].lower() or "elementwise" in r["Kernel_Name"])
+
+    cf, cw = copyk(pmc(prof + "/cal_fetch")), copyk(pmc(prof + "/cal_write"))
+    sf, sw = 1024 * 1024 / cf, 1024 * 1024 / cw          # 1 GiB in KiB / counter
+
+    def dec_rows(rows):
+        rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+        steps, cur = [], None
+        for r in rows:
+            if "pack_batch_kernel" in r["Kernel_Name"]:
+                cur = []
+                steps.append(cur)
+            if cur is not None:
+                cur.append(r)
+        dec = [s for s in steps[:-1] if not has_prompt(s)][1:]
+        return [(name, float(r["Counter_Value"])) for s in dec for r, name in dec_launches(s)]
+
+    fr, wr = dec_rows(pmc(prof + "/pmc_fetch")), dec_rows(pmc(prof + "/pmc_write"))
+    if len(fr) != len(wr) or any(a[0] != b[0] for a, b in zip(fr, wr)):
+        raise ValueError("the FETCH_SIZE and WRITE_SIZE runs dispatched different decode launches")
+    per = collections.defaultdict(lambda: [0, 0.0, 0.0])
+    for (name, a), (_, b) in zip(fr, wr):
+        p = per[name]
+        p[0] += 1
+        p[1] += a * 1024 * sf
+        p[2] += b * 1024 * sw
+    out = _header("HBM traffic of q4k_dec_kernel (decode-shaped Q4_K matmul), 8B-shape engine, B=16",
+                  ["pmc_fetch", "pmc_write", "cal_fetch", "cal_write"], [
+        "Each counter in its own run.  Counters are KiB per dispatch; each is scaled by what it reads for a",
+        "plain 1 GiB device copy (torch copy_, 1 GiB read + 1 GiB written).  Launches: the q4k_dec_kernel",
+        "dispatches of the decode-only steps (shape from the position in the step: QKV, O, gate+up, down per",
+        "layer, then the LM head).  traffic = fetch + write; 'alg' = algorithmic bytes.  Extra traffic over",
+        "'alg': split-K partial writes and one fetch of the activation operand per XCD.\n",
+        f"copy-kernel calibration: FETCH_SIZE {cf:.0f} KiB, WRITE_SIZE {cw:.0f} KiB per 1 GiB copy -> scale "
+        f"read x{sf:.4f}, write x{sw:.4f}",
+        "shape                    launches  fetch MB  write MB traffic MB   alg MB traffic/alg"])
+    tl = ta = tc = 0
+    for name in DEC_SHAPES:
+        c, a, b = per[name]
+        if not c:
+            continue
+        fa, wb, al = a / c, b / c, dec_alg_bytes(name)
+        out.append(f"{name:24s} {c:8d} {fa / 1e6:9.2f} {wb / 1e6:9.2f} {(fa + wb) / 1e6:10.2f} {al / 1e6:8.2f} "
+                   f"{(fa + wb) / al:11.3f}")
+        tl += a + b
+        ta += al * c
+        tc += c
+    out.append(f"all decode-step launches: {tc}, mean traffic {tl / tc / 1e6:.2f} MB, mean algorithmic "
+               f"{ta / tc / 1e6:.2f} MB, ratio {tl / ta:.3f}")
+    out.append(f"traffic_bytes_per_launch: {tl / tc:.0f}")
+    return "q4k_dec_traffic.txt", out
+
+
+def summary_ops(prof):
+    o = json.load(open(prof + "/ops.json"))
+    out = _header("Op-level figures: Q4_K and Q8_0 matmuls through the C ABI (C2) and ragged GQA attention (C3), "
+                  "MI355X", ["ops", "ops_trace"], [
+        "Per call: device time of a captured graph of many calls / calls (the table comes from the run without",
+        "the tracer).  Weights rotate over > 300 MB of copies (the Infinity Cache holds 256 MB); algorithmic",
+        "bytes = weights + 4*B*K + 4*B*M; ragged attention bytes = K/V once per kv head and sequence + q in and",
+        "out.", f"Measured 1 GiB device copy: {o['hbm_copy_GBs']:.0f} GB/s (nominal 8000).\n"])
+    if o.get("q4k_row_B1"):
+        out.append("q4k, one activation row on slate's row layout (the vtable's matvec_q4k):")
+        out.append("          M      K   B  us/call     GB/s of 8 TB/s")
+        for r in o["q4k_row_B1"]:
+            out.append(f"       {r['M']:6d} {r['K']:6d} {r['B']:3d} {r['us']:8.2f} {r['GBs']:8.1f} {r['frac_hbm']:9.3f}")
+        out.append("")
+    for fmt in ("q4k", "q8_0"):
+        out.append(f"{fmt} (tiled weights):      M      K   B  us/call     GB/s of 8 TB/s  TFLOP/s")
+        for r in o[fmt]:
+            out.append(f"                     {r['M']:6d} {r['K']:6d} {r['B']:3d} {r['us']:8.2f} {r['GBs']:8.1f} "
+                       f"{r['frac_hbm']:9.3f} {r['TFLOPs']:8.1f}")
+        out.append("")
+    a = o["attention"]
+    out.append(f"ragged attention B={a['B']} Hq={a['Hq']} Hkv={a['Hkv']} hd={a['head_dim']}, lengths "
+               "clip(round(exp(N(ln 1024, 1))), 16, 16384):")
+    out.append(f"  sum_L={a['sum_L']} max_L={a['max_L']}: {a['us']:.1f} us/call, {a['GBs']:.1f} GB/s "
+               f"({a['frac_hbm']:.3f} of 8 TB/s)")
+    out.append("\nrocprofv3 --stats of the --ops run (tracer durations):")
+    out += stats_lines(prof + "/ops_trace")
+    return "ops_q4k_c2_attention_c3.txt", out
+
+
+def summary_c5(prof):
+    steps = trace_steps(prof + "/trace70")
+    res = json.loads(open(prof + "/trace70.json").read().strip().splitlines()[-1])
+    n = len(steps)
+    body = steps[n // 3:]                       # after the warm-up has filled the batch
+    out = _header("Serving steps, 70B-shape Q4_K engine (80 layers, d 8192, 64q/8kv, SwiGLU 28672), Poisson "
+                  "arrivals (MI355X, one GPU)", ["trace70"], [
+        "Steps split at each pack_batch_kernel; the last two thirds of the run (the batch has filled).",
+        f"Run under the tracer: {res['steps']} timed steps, {res['value']} generated tok/s, "
+        f"{res['config'].get('prompt_tok_s', '?')} prompt tok/s.\n",
+        f"steps analysed: {len(body)} of {n}"])
+    b, _ = step_breakdown(body, 14)
+    out += b
+    out.append("\nrocprofv3 --stats over the whole run:")
+    out += stats_lines(prof + "/trace70")
+    return "serving_70b_c5_kernels.txt", out
+
+
+def summarize(prof):
+    """Write every profiles/ summary whose inputs exist under prof."""
+    made = 0
+    for fn in (summary_decode, summary_prefill, summary_traffic, summary_ops, summary_c5):
+        try:
+            name, lines = fn(prof)
+        except (FileNotFoundError, StopIteration, KeyError) as e:
+            log(f"{fn.__name__}: skipped ({e})")
+            continue
+        with open(os.path.join(ROOT, "profiles", name), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        log(f"wrote profiles/{name}")
+        made += 1
+    return 0 if made else 1
 
 
 if __name__ == "__main__":

@@ -70,6 +70,7 @@ struct Knobs {
     int q4k_wgs = 448;     // SLATE_HIP_Q4K_WGS: decode workgroup target of the plan
     int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
     int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one
+    int q4k_early = 1;     // SLATE_HIP_Q4K_EARLY=0: the decode kernel issues block 1 only after block 0 landed
     int q8_r = 0;          // SLATE_HIP_Q8_R, _S, _WGS: the same for the Q8_0 matmul
     int q8_s = 0;
     int q8_wgs = 448;

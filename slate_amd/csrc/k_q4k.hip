@@ -204,7 +204,7 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
 template <int R, bool TILED, int WAVES = 4, int NT = 1>
 __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, const uint4* frag,
                                                              float* __restrict__ out, int64_t ldo,
-                                                             int64_t split_stride, int nblk, int bps) {
+                                                             int64_t split_stride, int nblk, int bps, int early) {
     __shared__ uint4 s_act[2 * NT * ACT_FRAG_UNITS];
     constexpr int TCH = ACT_FRAG_UNITS / 64;          // 1 KiB wave copies per tile and block
     constexpr int CHUNKS = NT * TCH;
@@ -258,18 +258,32 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    // With `early` (and two blocks or more) the first two blocks go out
+    // together: both blocks' activation units, then block 0's weights, then
+    // block 1's; the first wait leaves block 1's weight loads in flight
+    // (loads complete in order), so their latency overlaps block 0's
+    // arithmetic instead of following it.
+    const bool two = early && nb > 1;
     stage(s_act, kb0);
+    if (two) stage(s_act + NT * ACT_FRAG_UNITS, kb0 + 1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
     __builtin_amdgcn_sched_barrier(0);
-    SH_WAIT_VMCNT(0);
+    if (two) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(w1[r], r, kb0 + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        SH_WAIT_VMCNT(3 * R);
+    } else {
+        SH_WAIT_VMCNT(0);
+    }
     __syncthreads();
     // block b from wc (landed) while wn receives block b+1; the two register
     // sets swap roles each step (the loop is unrolled by two)
     auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
         const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
-        if (b + 1 < nb) {                               // the last block prefetches nothing
+        if (b + 1 < nb && !(two && b == 0)) {           // the last block prefetches nothing
             stage(s_act + ((b + 1) & 1) * NT * ACT_FRAG_UNITS, kb0 + b + 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -560,15 +574,20 @@ template <int R, bool TILED>
 static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t ldo, int64_t ss, int nblk,
                        int bps, int nsplit, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     const int W = dec_waves();
+    const int early = knobs().q4k_early;
     const dim3 grid((tg.grp_end + W - 1) / W, nsplit);
     const uint4* fr = (const uint4*)a.frag;
     if (a.rows_pad == 32) {
-        if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 2>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps);
-        else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 2>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps);
+        if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 2>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps,
+                  early);
+        else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 2>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps,
+                  early);
         return;
     }
-    if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 1>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps);
-    else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 1>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps);
+    if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 1>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps,
+                  early);
+    else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 1>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps,
+                  early);
 }
 
 constexpr int PF_R = 2, PF_WAVES = 8;
