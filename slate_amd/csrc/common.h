@@ -71,6 +71,7 @@ struct Knobs {
     int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
     int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one
     int q4k_early = 1;     // SLATE_HIP_Q4K_EARLY=0: the decode kernel issues block 1 only after block 0 landed
+    int gemv1 = 1;         // SLATE_HIP_GEMV1=0: one-row C-ABI matvecs of tiled weights on the vector-ALU GEMV
     int q8_r = 0;          // SLATE_HIP_Q8_R, _S, _WGS: the same for the Q8_0 matmul
     int q8_s = 0;
     int q8_wgs = 448;
@@ -158,6 +159,11 @@ constexpr int GEMV_MAX_ROWS = 4;
 // the MFMA operand, so from two rows on the one-kernel GEMV no longer beats
 // the three-kernel MFMA path (operand conversion, matmul, split sum).
 constexpr int GEMV_ROUTE_ROWS = 1;
+// One activation row on MFMA over TILED weights (k_q4k.hip): one kernel, K
+// up to 64 blocks.
+constexpr int GEMV1_MAX_BLOCKS = 64;
+int launch_q4k_gemv1(const void* W, int M, int K, const float* x, float* y, hipStream_t s,
+                     hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64_t ldx, int B, int K, float* Y,
                     int64_t ldy, hipStream_t s, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 // TILED weight layout (16-row tiles, see k_q4k.hip).

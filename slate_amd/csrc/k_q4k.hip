@@ -10,6 +10,7 @@
 #include <algorithm>
 
 #include "launch.h"
+#include "lanes.h"
 #include "act16.h"
 #include "mfma.h"
 #include "q4k.h"
@@ -356,6 +357,156 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
                 for (int i = 0; i < 4; ++i) o[(int64_t)(16 * n + 4 * g + i) * ldo + row] = acc[r][n][i];
         }
     }
+}
+
+// One-row matvec on MFMA over TILED weights (slate_q4_k_matvec,
+// quant.c:306-313, for a single activation row; K up to GV1_MAXB blocks).
+// A workgroup owns one 16-row weight tile and all of K; wave w takes blocks
+// w, w + 8, ... and issues every one of its weight loads before anything
+// else.  Meanwhile it turns
+// the same blocks of x into the activation operand in LDS (per 256-element
+// block a power-of-two scale s, x*s = hi + lo in f16, the order act16.h
+// gives a lane group's eight values of a K step) and the f32 sub-block sums
+// of x.  The A operand of every MFMA is x in all 16 rows (each lane group
+// reads the same 16 bytes: an LDS broadcast), so each output row of the
+// 16x16 result holds the same dot product and a lane's first element is its
+// weight row's partial.  The block's min term dmin * sum_s mn_s * sum x_s
+// runs on the vector ALUs from the row's header.  The eight waves' partials
+// are added through LDS in a fixed order, so results are deterministic, and
+// one kernel writes the final row: no operand buffer, no split-K partials,
+// and ~0.6 VALU operations per weight against ~2.8 for the vector-ALU GEMV
+// (measured per call at B = 1 on the tiled layout: 5.6 / 10.9 / 14.4 us at
+// 4096x4096 / 14336x4096 / 4096x14336 against 7.7 / 15.9 / 19.4 us).  On
+// slate's row layout the lanes' 16-byte pieces of 16 rows scatter over 32
+// cache lines per load and the vector-ALU GEMV, which reads whole rows,
+// stays faster (11.7 vs 12.2 us at 14336x4096, also with the row pieces
+// regrouped through LDS).
+constexpr int GV1_WAVES = 8;
+constexpr int GV1_MAXB = 64;                          // K <= 16384 (eight blocks per wave)
+
+// LDS of a workgroup for up to GV1_WAVES * BPW blocks: per block the 32 hi
+// and 32 lo units (16 bytes each), eight sub-block sums and 1/s; then the
+// waves' partials.
+__host__ __device__ constexpr size_t gemv1_lds_bytes(int bpw) {
+    return (size_t)GV1_WAVES * bpw * (32 * 16 * 2 + 8 * 4 + 4) + GV1_WAVES * 16 * 4;
+}
+
+template <int BPW>
+__global__ __launch_bounds__(64 * GV1_WAVES) void q4k_gemv1_kernel(const uint8_t* W, int M,
+                                                                    const float* __restrict__ x,
+                                                                    float* __restrict__ y, int nblk) {
+    __shared__ uint4 s_dyn[gemv1_lds_bytes(BPW) / 16];
+    uint4* s_hi = s_dyn;                                       // [nblk][32]: step * 4 + lane group
+    uint4* s_lo = s_hi + (size_t)nblk * 32;
+    float* s_xs = (float*)(s_lo + (size_t)nblk * 32);          // [nblk][8] sub-block sums of x
+    float* s_rs = s_xs + (size_t)nblk * 8;                     // [nblk] 1/s
+    float* s_red = s_rs + nblk;                                // [waves][16]
+    const int lane = threadIdx.x & 63;
+    const int j = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = blockIdx.x;
+    // every load of the wave first: its blocks' weights, then its blocks of x
+    WTile w[BPW];
+    float4 xv[BPW];
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int kb = wv + GV1_WAVES * i;
+        if (kb < nblk) load_wtile_tiled(w[i], W + ((size_t)tile * nblk + kb) * (16 * QBLOCK), lane);
+    }
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int kb = wv + GV1_WAVES * i;
+        if (kb < nblk) xv[i] = *(const float4*)(x + (size_t)kb * QK + 4 * lane);
+    }
+    // the activation operand of this wave's blocks (the act16.h layout of one
+    // row: lane l holds elements 4l .. 4l+3 of the block)
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int kb = wv + GV1_WAVES * i;
+        if (kb < nblk) {
+            const float4 v = xv[i];
+            const float mx = wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            int ex = 0;
+            if (mx > 0.f && isfinite(mx)) {
+                frexpf(mx, &ex);
+                ex = 15 - ex;
+                ex = ex > 100 ? 100 : (ex < -100 ? -100 : ex);
+            }
+            const float sc = ldexpf(1.0f, ex);
+            const float vv[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+            half4_t h, l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[e] = (_Float16)vv[e];
+                l[e] = (_Float16)(vv[e] - (float)h[e]);
+            }
+            const int unit = kb * 32 + ((lane >> 1) & 7) * 4 + g, off = 8 * (lane & 1);
+            *(half4_t*)((uint8_t*)&s_hi[unit] + off) = half4_t{h[0], h[2], h[1], h[3]};
+            *(half4_t*)((uint8_t*)&s_lo[unit] + off) = half4_t{l[0], l[2], l[1], l[3]};
+            const float sum = group8_sum((v.x + v.y) + (v.z + v.w));
+            if ((lane & 7) == 0) s_xs[kb * 8 + (lane >> 3)] = sum;
+            if (lane == 0) s_rs[kb] = ldexpf(1.0f, -ex);
+        }
+    }
+    // this wave's blocks only read what this wave wrote: no barrier
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i) {
+        const int kb = wv + GV1_WAVES * i;
+        if (kb < nblk) {
+            const WScale cs = q4k_wscale(w[i], g);
+            floatx4 am = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const half8_t b = q4k_bop(w[i], cs, t);
+                const half8_t ah = __builtin_bit_cast(half8_t, s_hi[kb * 32 + t * 4 + g]);
+                const half8_t al = __builtin_bit_cast(half8_t, s_lo[kb * 32 + t * 4 + g]);
+                am = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, am, 0, 0, 0);
+                am = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, am, 0, 0, 0);
+            }
+            // min term of weight row j from its header: dmin * sum_s mn_s * sum x_s
+            const ScaleBytes sb = unpack_scales(w[i].hdr.y, w[i].hdr.z, w[i].hdr.w);
+            const float4 xa = *(const float4*)&s_xs[kb * 8], xb = *(const float4*)&s_xs[kb * 8 + 4];
+            const float mn = (float)(sb.mn_lo & 255u) * xa.x + (float)((sb.mn_lo >> 8) & 255u) * xa.y +
+                             (float)((sb.mn_lo >> 16) & 255u) * xa.z + (float)(sb.mn_lo >> 24) * xa.w +
+                             (float)(sb.mn_hi & 255u) * xb.x + (float)((sb.mn_hi >> 8) & 255u) * xb.y +
+                             (float)((sb.mn_hi >> 16) & 255u) * xb.z + (float)(sb.mn_hi >> 24) * xb.w;
+            acc += cs.d * am[0] * s_rs[kb] - cs.dmin64 * (1.0f / 64.0f) * mn;
+        }
+    }
+    if (g == 0) s_red[wv * 16 + j] = acc;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < GV1_WAVES; ++k) v += s_red[k * 16 + threadIdx.x];
+        const int row = tile * 16 + (int)threadIdx.x;
+        if (row < M) y[row] = v;
+    }
+}
+
+template <int BPW>
+static void launch_gemv1_t(dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1, const uint8_t* W, int M,
+                           const float* x, float* y, int nblk) {
+    SH_LAUNCH(e0, e1, (q4k_gemv1_kernel<BPW>), grid, dim3(64 * GV1_WAVES), 0, s, W, M, x, y, nblk);
+}
+
+int launch_q4k_gemv1(const void* W, int M, int K, const float* x, float* y, hipStream_t s, hipEvent_t ev_start,
+                     hipEvent_t ev_stop) {
+    const int nblk = K / QK;
+    if (M < 1 || K < QK || K % QK || nblk > GV1_MAXB) {
+        set_error(-1, "q4k_gemv1: M=%d, K=%d (K up to %d)", M, K, GV1_MAXB * QK);
+        return -1;
+    }
+    if ((uintptr_t)x & 15) { set_error(-1, "q4k_gemv1: the activation row must be 16-byte aligned"); return -1; }
+    const dim3 grid((M + 15) / 16);
+    const uint8_t* w = (const uint8_t*)W;
+    const int bpw = (nblk + GV1_WAVES - 1) / GV1_WAVES;
+    if (bpw <= 2) launch_gemv1_t<2>(grid, s, ev_start, ev_stop, w, M, x, y, nblk);
+    else if (bpw <= 4) launch_gemv1_t<4>(grid, s, ev_start, ev_stop, w, M, x, y, nblk);
+    else launch_gemv1_t<8>(grid, s, ev_start, ev_stop, w, M, x, y, nblk);
+    SH_CHECK_LAUNCH();
+    return 0;
 }
 
 // Prefill kernel (several 16-row activation tiles).  A workgroup of WAVES

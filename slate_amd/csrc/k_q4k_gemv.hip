@@ -176,6 +176,11 @@ int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64
     if (K < QK || K % QK) { set_error(-1, "q4k_gemv: K=%d", K); return -1; }
     if (((uintptr_t)X & 15) || ldx % 4) { set_error(-1, "q4k_gemv: activation rows must be 16-byte aligned"); return -1; }
     const int nblk = K / QK;
+    // one row of one tiled tensor: the MFMA matvec (SLATE_HIP_GEMV1=0 keeps
+    // this kernel; slate's row layout always stays here, where whole rows
+    // load contiguously)
+    if (B == 1 && n == 1 && tiled && t[0].col == 0 && nblk <= GEMV1_MAX_BLOCKS && knobs().gemv1)
+        return launch_q4k_gemv1(t[0].w, t[0].M, K, X, Y, s, ev_start, ev_stop);
     // rows per workgroup: 8 for one or two activation rows, 4 for three or
     // four (keeps the activations, 32 x B floats per thread, and the loads
     // of all R rows under 256 VGPRs: two waves per SIMD); one row of slate's

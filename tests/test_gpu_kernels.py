@@ -113,10 +113,16 @@ def test_matmul_q4k_c2_shapes(hip, orc, M, K):
         check(hip.matmul_q4k(Yr.p, Wd.p, Xd.p, B, M, K), "matmul_q4k")
         check(hip.lib.slate_hip_matmul_q4k_tiled(Yt.p, T.p, Xd.p, B, M, K), "matmul_q4k_tiled")
         got, gt = host(Yr, np.float32, (B, M)), host(Yt, np.float32, (B, M))
-        assert np.array_equal(bits(got), bits(gt)), B
-        assert relerr(got, orc.q4k_matmul(raw, X, M, K)) < 1e-5, B
+        want = orc.q4k_matmul(raw, X, M, K)
         ref = X.astype(np.float64) @ deq.T
-        assert np.all(np.abs(got - ref) <= 1e-4 * np.abs(ref) + 1e-5 * np.abs(ref).max()), B
+        # one row: the vector-ALU GEMV on the row layout, the MFMA matvec on
+        # the tiled one (each against the oracle); more rows: one kernel, the
+        # same bits from either layout
+        for y in ((got, gt) if B == 1 else (got,)):
+            assert relerr(y, want) < 1e-5, B
+            assert np.all(np.abs(y - ref) <= 1e-4 * np.abs(ref) + 1e-5 * np.abs(ref).max()), B
+        if B > 1:
+            assert np.array_equal(bits(got), bits(gt)), B
 
 
 @pytest.mark.parametrize("M,K", [(1, 256), (37, 256), (100, 16640), (257, 2304)])
@@ -124,9 +130,10 @@ def test_matmul_q4k_c2_shapes(hip, orc, M, K):
 def test_matmul_q4k_small_batch_edges(hip, orc, M, K, B):
     """Small batches at the edges of the kernels' tilings: one super-block
     (in the one-row GEMV a single wave with 8 busy lanes), row counts that
-    leave a partial workgroup, K above 64 super-blocks (two GEMV passes) and
-    K not a multiple of 2048; row and tiled layouts bit for bit, against
-    the oracle."""
+    leave a partial workgroup, K above 64 super-blocks (two GEMV passes; the
+    tiled layout's one-row MFMA matvec stops at 64) and K not a multiple of
+    2048; against the oracle, and row and tiled layouts bit for bit from two
+    rows on."""
     rng = np.random.default_rng(M * 13 + K + B)
     raw = np.frombuffer(quantize_q4k(rng.normal(0, 0.02, (M, K)).astype(np.float32)), np.uint8).copy()
     X = rng.normal(0, 1, (B, K)).astype(np.float32)
@@ -137,11 +144,14 @@ def test_matmul_q4k_small_batch_edges(hip, orc, M, K, B):
     Yr, Yt = DB(B * M * 4), DB(B * M * 4)
     check(hip.matmul_q4k(Yr.p, Wd.p, Xd.p, B, M, K), "matmul_q4k")
     check(hip.lib.slate_hip_matmul_q4k_tiled(Yt.p, T.p, Xd.p, B, M, K), "matmul_q4k_tiled")
-    got = host(Yr, np.float32, (B, M))
-    assert np.array_equal(bits(got), bits(host(Yt, np.float32, (B, M))))
+    got, gt = host(Yr, np.float32, (B, M)), host(Yt, np.float32, (B, M))
     want = orc.q4k_matmul(raw, X, M, K)
     for r in range(B):
         assert relerr(got[r], want[r]) < 1e-5, r
+    if B == 1:   # the tiled layout's MFMA matvec (K up to 64 blocks)
+        assert relerr(gt[0], want[0]) < 1e-5
+    else:
+        assert np.array_equal(bits(got), bits(gt))
     if B == 1:   # the vtable entry (backend.h:63-70) is the same kernel
         y = DB(M * 4)
         hip.matvec_q4k(y.p, Wd.p, Xd.p, M, K)
@@ -176,6 +186,21 @@ def test_matmul_q4k_activation_scales(hip, orc):
             if r < n:
                 assert relerr(got[r], want[r]) < 1e-5, (B, r)
         assert np.all(got[2] == 0)
+    # one row at a time, both layouts (the tiled layout's MFMA matvec scales
+    # each block of x itself)
+    Wd = dev(raw)
+    T = DB(hip.lib.slate_hip_q4k_tiled_bytes(M, K))
+    check(hip.lib.slate_hip_q4k_tile(T.p, Wd.p, M, K), "q4k_tile")
+    for r in range(6):
+        Y, Yt = DB(M * 4), DB(M * 4)
+        Xr = dev(X[r:r + 1])
+        check(hip.matmul_q4k(Y.p, Wd.p, Xr.p, 1, M, K), "matmul_q4k")
+        check(hip.lib.slate_hip_matmul_q4k_tiled(Yt.p, T.p, Xr.p, 1, M, K), "matmul_q4k_tiled")
+        for got in (host(Y, np.float32, (1, M)), host(Yt, np.float32, (1, M))):
+            if r == 2:
+                assert np.all(got == 0)
+            else:
+                assert relerr(got, orc.q4k_matmul(raw, X[r:r + 1], M, K)) < 1e-5, r
 
 
 def untile_q4k(t, M, K):
@@ -213,7 +238,9 @@ def test_q4k_tile_layout(hip, M, K):
                                    (6144, 4096, 16), (300, 1024, 40), (4096, 4096, 64)])
 def test_matmul_q4k_tiled(hip, orc, M, K, B):
     """The tiled layout gives the same results as the row layout, bit for
-    bit (same kernels and plan, only the weight addressing differs)."""
+    bit from two rows on (same kernels and plan, only the weight addressing
+    differs); one row runs the MFMA matvec on the tiled layout and the
+    vector-ALU GEMV on the row layout, both against the oracle."""
     rng = np.random.default_rng(M * 5 + K + B)
     W = rng.normal(0, 0.02, (M, K)).astype(np.float32)
     raw = np.frombuffer(quantize_q4k(W), np.uint8).copy()
@@ -225,9 +252,11 @@ def test_matmul_q4k_tiled(hip, orc, M, K, B):
     check(hip.lib.slate_hip_matmul_q4k_tiled(Yt.p, T.p, Xd.p, B, M, K), "matmul_q4k_tiled")
     check(hip.matmul_q4k(Yr.p, dev(raw).p, Xd.p, B, M, K), "matmul_q4k")
     got, row = host(Yt, np.float32, (B, M)), host(Yr, np.float32, (B, M))
-    assert np.array_equal(bits(got), bits(row))
-    if M * K <= 4096 * 4096 and B <= 16:
-        assert relerr(got, orc.q4k_matmul(raw, X, M, K)) < 1e-5
+    if B > 1:
+        assert np.array_equal(bits(got), bits(row))
+    if B == 1 or (M * K <= 4096 * 4096 and B <= 16):
+        want = orc.q4k_matmul(raw, X, M, K)
+        assert relerr(got, want) < 1e-5 and relerr(row, want) < 1e-5
 
 
 def test_matvec_q4k_vtable_golden(hip, golden):
