@@ -19,6 +19,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -99,8 +100,8 @@ struct slate_hip_llama {
     bool step_one_each = false;    // every sequence of the step adds exactly one token
     Knobs knobs;                   // kernel-path switches, read at creation (every step runs under them)
     // The decode attention's in-kernel merge is turned off for this engine
-    // once a launch reported a workgroup on another XCD than its queue's.
-    bool xcd_off = false;
+    // once a merge found a partial written on another XCD.
+    std::atomic<bool> xcd_off{false};
     float* h_logits = nullptr;
     std::vector<int> free_slots;
     std::vector<void*> allocs;
@@ -737,7 +738,7 @@ bool prompt_mfma_pays(const slate_hip_llama* m, slate_hip_llama_session_t* const
 // Enqueue one step (replaying the batch size's graph for decode-only
 // steps when graphs are on), wait for it and fold in its profile.
 int run_step(slate_hip_llama* m, int n, int T, bool want, hipStream_t s) {
-    m->h_status[1] = 0;   // set by the decode attention on a misplaced workgroup
+    m->h_status[1] = 0;   // set by a decode attention merge that found a partial from another XCD
     int rc;
     // decode-only steps repeat the same launch sequence for a given batch
     // size: replay it as a HIP graph (the descriptor copy in the graph reads
@@ -1106,11 +1107,12 @@ int slate_hip_llama_step(slate_hip_llama_t* m, slate_hip_llama_session_t** sessi
         if (m->h_status[1] != 0) {
             // A merge inside the decode attention found a partial of its pair
             // written on another XCD, so it may have read what that XCD's L2
-            // still held: the step's results are not trusted.  Turn the in-kernel merge off for this engine
-            // and run the step again on the merge kernel.  Running it again
-            // is exact: a step recomputes everything from its tokens and the
-            // K/V rows before its positions, and rewrites the rows at its
-            // positions with the same values.
+            // still held: the step's results are not trusted.  Turn the
+            // in-kernel merge off for this engine and run the step again on
+            // the merge kernel.  Running it again is exact: a step recomputes
+            // everything from its tokens and the K/V rows before its
+            // positions, and rewrites the rows at its positions with the same
+            // values.
             m->xcd_off = true;
             for (const auto& g : m->graphs) (void)hipGraphExecDestroy(g.exec);
             m->graphs.clear();
