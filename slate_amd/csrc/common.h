@@ -72,6 +72,7 @@ struct Knobs {
     int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one
     int q4k_early = 1;     // SLATE_HIP_Q4K_EARLY=0: the decode kernel issues block 1 only after block 0 landed
     int gemv1 = 1;         // SLATE_HIP_GEMV1=0: one-row C-ABI matvecs of tiled weights on the vector-ALU GEMV
+    int row_pad64 = 0;     // SLATE_HIP_ROW_PAD64=1: rows beyond 64 padded to multiples of 64, not 16
     int q8_r = 0;          // SLATE_HIP_Q8_R, _S, _WGS: the same for the Q8_0 matmul
     int q8_s = 0;
     int q8_wgs = 448;
@@ -170,9 +171,13 @@ int launch_q4k_gemv(const Q4kTarget* t, int n, bool tiled, const float* X, int64
 size_t q4k_tiled_bytes(int M, int K);
 int launch_q4k_tile(void* dst, const void* src, int M, int K, hipStream_t s);
 void q4k_untile_host(uint8_t* dst, const uint8_t* src, int M, int K);
-// Activation rows are padded to whole 16-row MFMA tiles, and to whole groups
-// of four tiles beyond 64 rows, so every launch uses a single tile count.
-inline int row_pad(int rows) { return rows <= 64 ? (rows + 15) / 16 * 16 : (rows + 63) / 64 * 64; }
+// Activation rows are padded to whole 16-row MFMA tiles (the prompt kernels
+// take a last group of fewer tiles than the others and skip the missing
+// ones); SLATE_HIP_ROW_PAD64=1 pads rows beyond 64 to whole groups of four
+// tiles instead.
+inline int row_pad(int rows) {
+    return knobs().row_pad64 && rows > 64 ? (rows + 63) / 64 * 64 : (rows + 15) / 16 * 16;
+}
 // Carve an Act16 for B rows x K out of backend scratch slot `slot`.
 int make_act16(Act16& a, int B, int K, int slot);
 

@@ -541,6 +541,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     const int tile0 = ((wg - wg0) * WAVES + wv) * R;
     const bool active = tile0 < tiles;
     const int at0 = blockIdx.z * NT;
+    const int nt = min(NT, act_tiles - at0);          // >= 1; the last group may hold fewer tiles
     const int kb0 = blockIdx.y * bps;
     const int nb = min(kb0 + bps, nblk) - kb0;        // >= 1: the launcher sizes the grid
     const uint8_t* wp[R];
@@ -627,6 +628,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
                 }
 #pragma unroll
                 for (int n = 0; n < NT; ++n) {
+                    if (n >= nt) break;                    // workgroup-uniform
                     const uint4* sa = cur + n * ACT_FRAG_UNITS;
                     const half8_t h = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
                     const half8_t l = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
@@ -643,6 +645,7 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
             }
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
+                if (n >= nt) break;
                 const uint4* sa = cur + n * ACT_FRAG_UNITS;
                 const half4_t ys = *(const half4_t*)(sa + 1024 + lane);
                 const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
