@@ -195,7 +195,7 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
 // workgroup of WAVES waves owns WAVES*R weight tiles (possibly spread over
 // up to three fused tensors) and one split of super-blocks.  The NT tiles'
 // activation units of a block are copied into a double-buffered LDS area by
-// direct global->LDS loads, one block ahead and issued before the next
+// direct global->LDS loads, one block ahead and issued after the next
 // block's weight loads; each wave holds its R weight tiles in registers,
 // loaded one block ahead, and builds each tile's B operand once per K step
 // for all NT activation tiles; every step ends with one wait for all loads
@@ -259,38 +259,9 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // With `early` (and two blocks or more) the first two blocks go out
-    // together: both blocks' activation units, then block 0's weights, then
-    // block 1's; the first wait leaves block 1's weight loads in flight
-    // (loads complete in order), so their latency overlaps block 0's
-    // arithmetic instead of following it.
-    const bool two = early && nb > 1;
-    stage(s_act, kb0);
-    if (two) stage(s_act + NT * ACT_FRAG_UNITS, kb0 + 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
-    __builtin_amdgcn_sched_barrier(0);
-    if (two) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) ldw(w1[r], r, kb0 + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        SH_WAIT_VMCNT(3 * R);
-    } else {
-        SH_WAIT_VMCNT(0);
-    }
-    __syncthreads();
-    // block b from wc (landed) while wn receives block b+1; the two register
-    // sets swap roles each step (the loop is unrolled by two)
-    auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
-        const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
-        if (b + 1 < nb && !(two && b == 0)) {           // the last block prefetches nothing
-            stage(s_act + ((b + 1) & 1) * NT * ACT_FRAG_UNITS, kb0 + b + 1);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int r = 0; r < R; ++r) ldw(wn[r], r, kb0 + b + 1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+    // a block's products from the landed weights wc and operand buffer slot
+    auto compute = [&](const WTile (&wc)[R], int slot) {
+        const uint4* cur = s_act + slot * NT * ACT_FRAG_UNITS;
         if (active) {
             // one K step at a time: each tile's B operand is built once and
             // run against the NT activation fragments of the step
@@ -335,16 +306,64 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
                 }
             }
         }
+    };
+    // block b (< nb): weights into w, operand units into buffer b & 1
+    auto issue = [&](WTile (&w)[R], int b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(w[r], r, kb0 + b);
         __builtin_amdgcn_sched_barrier(0);
-        SH_WAIT_VMCNT(0);                              // next block's units and weights have landed
+        stage(s_act + (b & 1) * NT * ACT_FRAG_UNITS, kb0 + b);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // block b from wc (landed) while wn receives block b+1; the two register
+    // sets swap roles each step (the loop is unrolled by two).  Every step
+    // ends with one wait for all loads and one barrier.
+    auto step = [&](const WTile (&wc)[R], WTile (&wn)[R], int b) {
+        if (b + 1 < nb) issue(wn, b + 1);            // the last block prefetches nothing
+        compute(wc, b & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        SH_WAIT_VMCNT(0);                              // block b+1's units and weights have landed
         __syncthreads();
     };
-    int b = 0;
-    for (; b + 2 <= nb; b += 2) {
-        step(w0, w1, b);
-        step(w1, w0, b + 1);
+
+    // Block 0 is peeled off the loop, so that the loop starts with no load
+    // in flight on every path into it: the compiler then places no wait of
+    // its own inside the loop (a path into the loop with loads in flight
+    // makes it wait, in every step, for loads issued in that same step).
+    // With `early` block 1 goes out together with block 0 (its index
+    // clamped to the last block, so the loads are unconditional and the
+    // first wait has one count): both blocks' operand units, block 0's
+    // weights, then block 1's; the first wait leaves block 1's weight loads
+    // in flight (loads complete in order) while block 0 is computed.
+    if (early) {
+        const int b1 = nb > 1 ? 1 : 0;
+        stage(s_act, kb0);
+        stage(s_act + NT * ACT_FRAG_UNITS, kb0 + b1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(w1[r], r, kb0 + b1);
+        __builtin_amdgcn_sched_barrier(0);
+        SH_WAIT_VMCNT(3 * R);
+        __syncthreads();
+        compute(w0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        SH_WAIT_VMCNT(0);
+        __syncthreads();
+    } else {
+        issue(w0, 0);
+        SH_WAIT_VMCNT(0);
+        __syncthreads();
+        step(w0, w1, 0);
     }
-    if (b < nb) step(w0, w1, b);
+    int b = 1;
+    for (; b + 2 <= nb; b += 2) {
+        step(w1, w0, b);
+        step(w0, w1, b + 1);
+    }
+    if (b < nb) step(w1, w0, b);
     if (!active) return;
     float* o = out + (int64_t)blockIdx.y * split_stride + col;
 #pragma unroll
