@@ -1025,8 +1025,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_dec_rope_xcd_kernel(
     constexpr int NB = G * HD / 256;                   // operand blocks of a kv head's G heads
     __shared__ int s_last;
     const int xcc = blockIdx.x & 7, u = blockIdx.x >> 3;
-    if (u >= xq.len[xcc]) return;                      // workgroup-uniform
+    // the queue length and the unit are read together (one round trip);
+    // u < cap for every workgroup of the grid, so the unit read is in bounds
+    const int len = xq.len[xcc];
     const int4 d = xq.units[(size_t)xcc * xq.cap + u];
+    if (u >= len) return;                              // workgroup-uniform
     AttnUnit un;
     un.n = 0;
     un.t = d.x >> 16;
