@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "launch.h"
 #include "lanes.h"
@@ -573,8 +574,9 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
         if (TILED) load_wtile_tiled(w, wp[r] + (size_t)kb * (16 * QBLOCK), lane);
         else load_wtile(w, wp[r] + (size_t)kb * QBLOCK, g);
     };
-    // copy block kb of activation tiles at0 .. at0+NT-1 (clamped) into `dst`
-    // (every address stays inside the operand buffer: at < act_tiles, kb < nblk).
+    // chunks of block kb of activation tiles at0 .. at0+NT-1 (clamped; the
+    // last group copies only the tiles it holds): every address stays inside
+    // the operand buffer (at < act_tiles, kb < nblk).
     // The wave's chunks sit at fixed byte offsets from block kb's base (the
     // operand buffer of a prompt chunk is far below 4 GiB) and at fixed LDS
     // offsets, computed once: a copy costs one 64-bit scalar add and an m0 add.
@@ -590,117 +592,130 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
         csrc[i] = (uint32_t)(((uint32_t)at * (uint32_t)nblk * ACT_FRAG_UNITS + u) * 16u);
         clds[i] = (uint32_t)((n * ACT_FRAG_UNITS + u) * 16);
     }
-    auto stage = [&](uint4* dst, int kb) {
-        const char* sb = (const char*)(frag + (size_t)kb * ACT_FRAG_UNITS);
-        const uint32_t lb = lds_addr(dst);
+    // The block loop, specialised on the number NTA of activation tiles the
+    // workgroup holds (NT, or fewer in the last group along z): every loop
+    // over the tiles is unrolled with no branch inside the K steps, so the
+    // compiler issues the LDS reads of several tiles ahead of their MFMAs and
+    // interleaves the next step's B operands with them.  (A per-tile
+    // workgroup-uniform branch there splits each K step into one basic block
+    // per tile, and each tile's MFMAs then wait behind their own LDS reads.)
+    auto run = [&](auto ntag) {
+        constexpr int NTA = decltype(ntag)::value;
+        constexpr int CH_A = NTA * (ACT_FRAG_UNITS / 64);   // chunks of the NTA tiles
+        auto stage_a = [&](uint4* dst, int kb) {
+            const char* sb = (const char*)(frag + (size_t)kb * ACT_FRAG_UNITS);
+            const uint32_t lb = lds_addr(dst);
 #pragma unroll
-        for (int i = 0; i < NCH; ++i)
-            if (wv + WAVES * i < CHUNKS) lds_copy16(sb + csrc[i], o_act, lb + clds[i]);
-    };
-    WTile wc[R], wn[R];
-    floatx4 acc[R][NT];
+            for (int i = 0; i < NCH; ++i)
+                if (wv + WAVES * i < CH_A) lds_copy16(sb + csrc[i], o_act, lb + clds[i]);
+        };
+        WTile wc[R], wn[R];
+        floatx4 acc[R][NTA];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int n = 0; n < NT; ++n) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int n = 0; n < NTA; ++n) acc[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    stage(s_act, kb0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
-    __builtin_amdgcn_sched_barrier(0);
-    SH_WAIT_VMCNT(0);
-    __syncthreads();
-    // (swapping two register sets instead of copying, as the decode kernel
-    // does, costs this kernel 30 more VGPRs and 8 % at T = 320)
-    for (int b = 0; b < nb; ++b) {
-        // compute block b from one buffer while the other receives block b+1
-        const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
-        const int kn = kb0 + min(b + 1, nb - 1);
-        if (b + 1 < nb) stage(s_act + ((b + 1) & 1) * NT * ACT_FRAG_UNITS, kn);
+        stage_a(s_act, kb0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
+        for (int r = 0; r < R; ++r) ldw(wc[r], r, kb0);
         __builtin_amdgcn_sched_barrier(0);
-        if (active) {
-            // one K step at a time: each tile's B operand is built once and
-            // used against every activation tile, so consecutive MFMAs
-            // belong to independent accumulators
-            WScale cs[R];
-            floatx4 am[R][NT];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                cs[r] = q4k_wscale(wc[r], g);
-#pragma unroll
-                for (int n = 0; n < NT; ++n) am[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
-            }
-            // the B operands of K step t + 1 are built while step t's MFMAs run
-            half8_t bcur[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) bcur[r] = q4k_bop(wc[r], cs[r], 0);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                half8_t bnx[R];
-                if (t < 7) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) bnx[r] = q4k_bop(wc[r], cs[r], t + 1);
-                }
-#pragma unroll
-                for (int n = 0; n < NT; ++n) {
-                    if (n >= nt) break;                    // workgroup-uniform
-                    const uint4* sa = cur + n * ACT_FRAG_UNITS;
-                    const half8_t h = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
-                    const half8_t l = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bcur[r], am[r][n], 0, 0, 0);
-                        am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bcur[r], am[r][n], 0, 0, 0);
-                    }
-                }
-                if (t < 7) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) bcur[r] = bnx[r];
-                }
-            }
-#pragma unroll
-            for (int n = 0; n < NT; ++n) {
-                if (n >= nt) break;
-                const uint4* sa = cur + n * ACT_FRAG_UNITS;
-                const half4_t ys = *(const half4_t*)(sa + 1024 + lane);
-                const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
-                const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    floatx4 an = {0.f, 0.f, 0.f, 0.f};
-                    an = __builtin_amdgcn_mfma_f32_16x16x16f16(ys, cs[r].bmin, an, 0, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[r][n][i] += (cs[r].d * am[r][n][i] - cs[r].dmin64 * an[i]) * rs[i];
-                }
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // the next block's units and weights have landed: waiting for the
-        // weights here (not at their first use) keeps the compiler's in-order
-        // load counting from also waiting on the next step's LDS copies
         SH_WAIT_VMCNT(0);
         __syncthreads();
+        // (swapping two register sets instead of copying, as the decode kernel
+        // does, costs this kernel 30 more VGPRs and 8 % at T = 320)
+        for (int b = 0; b < nb; ++b) {
+            // compute block b from one buffer while the other receives block b+1
+            const uint4* cur = s_act + (b & 1) * NT * ACT_FRAG_UNITS;
+            const int kn = kb0 + min(b + 1, nb - 1);
+            if (b + 1 < nb) stage_a(s_act + ((b + 1) & 1) * NT * ACT_FRAG_UNITS, kn);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < R; ++r) wc[r] = wn[r];
-    }
-    if (!active) return;
-    float* o = out + (int64_t)blockIdx.y * split_stride + col;
+            for (int r = 0; r < R; ++r) ldw(wn[r], r, kn);
+            __builtin_amdgcn_sched_barrier(0);
+            if (active) {
+                // one K step at a time: each tile's B operand is built once and
+                // used against every activation tile, so consecutive MFMAs
+                // belong to independent accumulators
+                WScale cs[R];
+                floatx4 am[R][NTA];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = (tile0 + r) * 16 + j;
-        if (tile0 + r >= tiles || row >= M) continue;
+                for (int r = 0; r < R; ++r) {
+                    cs[r] = q4k_wscale(wc[r], g);
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            if (at0 + n >= act_tiles) break;
+                    for (int n = 0; n < NTA; ++n) am[r][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+                // the B operands of K step t + 1 are built while step t's MFMAs run
+                half8_t bcur[R];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[(int64_t)((at0 + n) * 16 + 4 * g + i) * ldo + row] = acc[r][n][i];
+                for (int r = 0; r < R; ++r) bcur[r] = q4k_bop(wc[r], cs[r], 0);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    half8_t bnx[R];
+                    if (t < 7) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r) bnx[r] = q4k_bop(wc[r], cs[r], t + 1);
+                    }
+#pragma unroll
+                    for (int n = 0; n < NTA; ++n) {
+                        const uint4* sa = cur + n * ACT_FRAG_UNITS;
+                        const half8_t h = __builtin_bit_cast(half8_t, sa[(2 * t) * 64 + lane]);
+                        const half8_t l = __builtin_bit_cast(half8_t, sa[(2 * t + 1) * 64 + lane]);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, bcur[r], am[r][n], 0, 0, 0);
+                            am[r][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, bcur[r], am[r][n], 0, 0, 0);
+                        }
+                    }
+                    if (t < 7) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r) bcur[r] = bnx[r];
+                    }
+                }
+#pragma unroll
+                for (int n = 0; n < NTA; ++n) {
+                    const uint4* sa = cur + n * ACT_FRAG_UNITS;
+                    const half4_t ys = *(const half4_t*)(sa + 1024 + lane);
+                    const float4 rv = __builtin_bit_cast(float4, sa[1088 + g]);
+                    const floatx4 rs = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        floatx4 an = {0.f, 0.f, 0.f, 0.f};
+                        an = __builtin_amdgcn_mfma_f32_16x16x16f16(ys, cs[r].bmin, an, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acc[r][n][i] += (cs[r].d * am[r][n][i] - cs[r].dmin64 * an[i]) * rs[i];
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // the next block's units and weights have landed: waiting for the
+            // weights here (not at their first use) keeps the compiler's in-order
+            // load counting from also waiting on the next step's LDS copies
+            SH_WAIT_VMCNT(0);
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < R; ++r) wc[r] = wn[r];
         }
-    }
+        if (!active) return;
+        float* o = out + (int64_t)blockIdx.y * split_stride + col;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = (tile0 + r) * 16 + j;
+            if (tile0 + r >= tiles || row >= M) continue;
+#pragma unroll
+            for (int n = 0; n < NTA; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[(int64_t)((at0 + n) * 16 + 4 * g + i) * ldo + row] = acc[r][n][i];
+        }
+    };
+    // nt is the same for the whole workgroup (blockIdx.z); the barriers
+    // inside run() are reached by every wave of it
+    if (nt >= NT) run(std::integral_constant<int, NT>{});
+    else if (nt == 1) run(std::integral_constant<int, 1>{});
+    else if (nt == 2) run(std::integral_constant<int, (NT > 2 ? 2 : 1)>{});
+    else run(std::integral_constant<int, (NT > 3 ? 3 : 1)>{});
 }
 
 // Decode plan: the largest R in {4, 2, 1}, then the fewest splits, that give
