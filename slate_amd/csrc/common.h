@@ -69,6 +69,7 @@ struct Knobs {
     int q4k_s = 0;         // SLATE_HIP_Q4K_S: decode split count (0 = plan)
     int q4k_wgs = 576;     // SLATE_HIP_Q4K_WGS: decode workgroup target of the plan
     int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
+    int q4k_pf_nt = 0;     // SLATE_HIP_Q4K_PF_NT: 2 or 4 activation tiles per prompt workgroup (0 = plan)
     int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one
     int q4k_early = 1;     // SLATE_HIP_Q4K_EARLY=0: the decode kernel issues block 1 only after block 0 landed
     int gemv1 = 1;         // SLATE_HIP_GEMV1=0: one-row C-ABI matvecs of tiled weights on the vector-ALU GEMV

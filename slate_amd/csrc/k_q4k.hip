@@ -843,9 +843,17 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
             const int slots = pf_slots(NT);
             int Sb = 1;
             double best = 1e30;
-            for (int c = 1; c <= 16 && c <= max_splits && c <= (nblk > 1 ? nblk / 2 : 1); c *= 2) {
+            // every split count the block ranges can give (c splits of
+            // ceil(nblk / c) blocks, the last one shorter), not only powers
+            // of two: at about 300 rows the 4096-row shapes fill one round
+            // with three splits, where two leave 96 CUs idle and four take
+            // two rounds
+            const int cmax = std::min(std::min(16, max_splits), nblk > 1 ? nblk / 2 : 1);
+            for (int c = 1; c <= cmax; ++c) {
+                const int bps_c = (nblk + c - 1) / c;
+                if ((nblk + bps_c - 1) / bps_c != c) continue;   // the same ranges as a smaller c
                 const int rounds = (tasks * c + slots - 1) / slots;
-                const double cost = (double)rounds * ((double)(nblk + c - 1) / c + 4.0);
+                const double cost = (double)rounds * ((double)bps_c + 4.0);
                 if (cost <= best + 1e-9) { best = cost; Sb = c; }   // ties: more splits (measured faster)
             }
             const int rem = tasks * Sb % slots;
@@ -868,6 +876,10 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         if (NT == 4 && rounds >= 2 && fill < 0.6) {
             NT = 2;
             S = plan(2, &fill, &rounds);
+        }
+        if ((knobs().q4k_pf_nt == 2 || knobs().q4k_pf_nt == 4) && knobs().q4k_pf_nt != NT) {
+            NT = knobs().q4k_pf_nt;
+            S = plan(NT, &fill, &rounds);
         }
         const int S_env = knobs().q4k_pf_s;
         if (S_env > 0) S = std::min(S_env, std::max(1, std::min(max_splits, nblk)));
