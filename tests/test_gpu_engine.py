@@ -543,14 +543,16 @@ def test_graph_replayed_decode_steps_match_eager_launches(golden):
         assert np.array_equal(K1, K2) and np.array_equal(V1, V2)
 
 
-def test_f16_kv_cache_tolerance_study(orc, monkeypatch):
-    """The opt-in f16 K/V cache against the oracle's f32 reference: a 512-wide
-    Q4_K model (head_dim 64), three prompts of 150-280 tokens (contexts over
-    two 256-key chunks), 24 ragged decode steps; every step's logits stay
-    within the parity tolerance (normwise relative 1e-3).  Layer 0's cached
-    K/V equal the f32 engine's rounded to f16 (layers above also carry the
-    f16 attention's own rounding)."""
-    shape = LlamaShape(2, 512, 8, 4, 768, 300, 512)
+@pytest.mark.parametrize("shape", [LlamaShape(2, 512, 8, 4, 768, 300, 512),
+                                   LlamaShape(2, 1024, 8, 2, 768, 300, 512)], ids=["hd64", "hd128"])
+def test_f16_kv_cache_tolerance_study(orc, monkeypatch, shape):
+    """The opt-in f16 K/V cache against the oracle's f32 reference: Q4_K
+    models with head_dim 64 (8 query / 4 KV heads) and 128 (8 / 2: the
+    16-byte f16 row loads, eight values per lane), three prompts of 150-280
+    tokens (contexts over two 256-key chunks), 24 ragged decode steps; every
+    step's logits stay within the parity tolerance (normwise relative 1e-3).
+    Layer 0's cached K/V equal the f32 engine's rounded to f16 (layers above
+    also carry the f16 attention's own rounding)."""
     t = make_llama(shape, 4321, quant="q4k", output_quant="q4k")
     rng = np.random.default_rng(16)
     prompts = [rng.integers(0, shape.vocab, n).astype(np.int32) for n in (150, 220, 280)]
