@@ -27,9 +27,11 @@ namespace slate_hip {
 
 typedef _Float16 act_half4_t __attribute__((ext_vector_type(4)));
 
-// One wave writes block kb of row r; lane holds elements 4*lane .. 4*lane+3
-// (zeros for padding rows).  Every lane of the wave must call it.
-__device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb, int lane, float4 v) {
+// One wave writes row rr (0..15) of the 16-row tile block whose units start
+// at fb (global memory, or an LDS copy of the same layout); lane holds
+// elements 4*lane .. 4*lane+3 (zeros for padding rows).  Every lane of the
+// wave must call it.
+__device__ __forceinline__ void act16_store_tile_row(uint8_t* fb, int rr, int lane, float4 v) {
     const float mx = wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     int ex = 0;
     if (mx > 0.f && isfinite(mx)) {
@@ -52,8 +54,6 @@ __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb,
     const _Float16 sh = (_Float16)ss;
     const _Float16 sl = (_Float16)(ss - (float)sh);
     const int sub = lane >> 3;
-    const int rr = r & 15;
-    uint8_t* fb = (uint8_t*)a.frag + ((size_t)(r >> 4) * (a.K / QK) + kb) * ACT_FRAG_UNITS * 16;
     const int g = lane >> 4, t = (lane >> 1) & 7, half_off = 8 * (lane & 1);
     const act_half4_t hp = {h[0], h[2], h[1], h[3]}, lp = {l[0], l[2], l[1], l[3]};
     *(act_half4_t*)(fb + ((2 * t) * 64 + 16 * g + rr) * 16 + half_off) = hp;
@@ -66,6 +66,12 @@ __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb,
         *(_Float16*)(fb + (1024 + 16 * (g0 + 2) + rr) * 16 + 2 * (sub & 3)) = sl;
     }
     if (lane == 0) *(float*)(fb + 1088 * 16 + 4 * rr) = ldexpf(1.0f, -ex);
+}
+
+// One wave writes block kb of row r of the operand a.
+__device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb, int lane, float4 v) {
+    uint8_t* fb = (uint8_t*)a.frag + ((size_t)(r >> 4) * (a.K / QK) + kb) * ACT_FRAG_UNITS * 16;
+    act16_store_tile_row(fb, r & 15, lane, v);
 }
 
 }  // namespace slate_hip

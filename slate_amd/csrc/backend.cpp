@@ -283,6 +283,18 @@ static int matmul_q4k_common(float* Y, const void* A, const float* X, int B, int
     // one row: one GEMV kernel straight into Y (no operand, no partials)
     if (B <= GEMV_ROUTE_ROWS && ((uintptr_t)X & 15) == 0)
         return launch_q4k_gemv(&t, 1, tiled, X, K, B, K, Y, M, g_stream);
+    if (B <= 16) {
+        // one activation tile: the matmul makes its operand from X itself,
+        // then the split sum (two kernels per call)
+        const int max_splits = 32;
+        float* part = (float*)scratch(1, (size_t)max_splits * 16 * M * sizeof(float));
+        if (!part) return -2;
+        int S = 1;
+        const int rc = launch_q4k_conv(t, tiled, X, K, B, K, part, (int64_t)M, (int64_t)16 * M, max_splits, &S,
+                                       g_stream);
+        if (rc < 0) return rc;
+        if (rc == 0) return launch_sum_splits(Y, part, S, B, 16, M, g_stream);
+    }
     Act16 a;
     if (make_act16(a, B, K, 0)) return -2;
     int rc = launch_act16_from_f32(a, X, K, g_stream);

@@ -150,6 +150,12 @@ struct Q4kTargets {                 // kernel-argument form
 int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out, int64_t ldo,
                int64_t split_stride, int max_splits, int* S_out, hipStream_t s,
                hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+// One tensor, 1 < rows <= 16 f32 rows of X (ldx floats apart): the split-K
+// partials of Y = X W^T in one launch that makes the activation operand
+// itself (rows padded to 16).  Returns 1 without launching when the decode
+// plan is not the 8-wave one (the caller then stages the operand).
+int launch_q4k_conv(const Q4kTarget& t, bool tiled, const float* X, int64_t ldx, int rows, int K, float* out,
+                    int64_t ldo, int64_t split_stride, int max_splits, int* S_out, hipStream_t s);
 // Small-batch Q4_K GEMV (k_q4k_gemv.hip): 1..GEMV_MAX_ROWS activation rows
 // X [B, K] f32 (16-byte aligned rows, ldx floats apart) against up to three
 // tensors (ROW or TILED layout); writes final rows Y[b * ldy + col + m] in

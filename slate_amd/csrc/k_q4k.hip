@@ -203,10 +203,20 @@ __device__ __forceinline__ half8_t q4k_bop(const WTile& w, const WScale& c, int 
 // and one barrier.  W and frag are not __restrict__: loads through restrict
 // pointers count as invariant and may be moved across the barriers that
 // order them here.
-template <int R, bool TILED, int WAVES = 4, int NT = 1>
+//
+// CONV (one activation tile; the C ABI's matmuls of 2-16 rows): the operand
+// is not read from a buffer but made in the kernel from the f32 rows X (ldx
+// floats apart, rows >= xrows zero): each wave loads two rows of the next
+// block into registers before computing the current one, and after it
+// writes them into the other LDS buffer in the operand layout (act16.h), the
+// same values the operand kernel would write.
+template <int R, bool TILED, int WAVES = 4, int NT = 1, bool CONV = false>
 __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, const uint4* frag,
                                                              float* __restrict__ out, int64_t ldo,
-                                                             int64_t split_stride, int nblk, int bps, int early) {
+                                                             int64_t split_stride, int nblk, int bps, int early,
+                                                             const float* X = nullptr, int64_t ldx = 0,
+                                                             int xrows = 0) {
+    static_assert(!CONV || (NT == 1 && WAVES == 8), "CONV: one activation tile, two rows per wave");
     __shared__ uint4 s_act[2 * NT * ACT_FRAG_UNITS];
     constexpr int TCH = ACT_FRAG_UNITS / 64;          // 1 KiB wave copies per tile and block
     constexpr int CHUNKS = NT * TCH;
@@ -336,7 +346,44 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
     // first wait has one count): both blocks' operand units, block 0's
     // weights, then block 1's; the first wait leaves block 1's weight loads
     // in flight (loads complete in order) while block 0 is computed.
-    if (early) {
+    if constexpr (CONV) {
+        // rows 2*wv, 2*wv + 1 of block kb into registers, then into buffer dst
+        float4 xr[2];
+        auto xload = [&](int kb) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = 2 * wv + i;
+                xr[i] = r < xrows ? *(const float4*)(X + (int64_t)r * ldx + (int64_t)kb * QK + 4 * lane)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        };
+        auto xstore = [&](uint4* dst) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) act16_store_tile_row((uint8_t*)dst, 2 * wv + i, lane, xr[i]);
+        };
+        xload(kb0);
+#pragma unroll
+        for (int r = 0; r < R; ++r) ldw(w0[r], r, kb0);
+        xstore(s_act);
+        SH_WAIT_VMCNT(0);
+        __syncthreads();
+        for (int b = 0; b < nb; ++b) {
+            const bool more = b + 1 < nb;
+            if (more) {
+                xload(kb0 + b + 1);
+#pragma unroll
+                for (int r = 0; r < R; ++r) ldw(w1[r], r, kb0 + b + 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            compute(w0, b & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) xstore(s_act + ((b + 1) & 1) * ACT_FRAG_UNITS);
+            SH_WAIT_VMCNT(0);
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < R; ++r) w0[r] = w1[r];
+        }
+    } else if (early) {
         const int b1 = nb > 1 ? 1 : 0;
         stage(s_act, kb0);
         stage(s_act + NT * ACT_FRAG_UNITS, kb0 + b1);
@@ -359,12 +406,14 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_dec_kernel(Q4kTargets tg, cons
         __syncthreads();
         step(w0, w1, 0);
     }
-    int b = 1;
-    for (; b + 2 <= nb; b += 2) {
-        step(w1, w0, b);
-        step(w0, w1, b + 1);
+    if constexpr (!CONV) {
+        int b = 1;
+        for (; b + 2 <= nb; b += 2) {
+            step(w1, w0, b);
+            step(w0, w1, b + 1);
+        }
+        if (b < nb) step(w1, w0, b);
     }
-    if (b < nb) step(w1, w0, b);
     if (!active) return;
     float* o = out + (int64_t)blockIdx.y * split_stride + col;
 #pragma unroll
@@ -767,15 +816,15 @@ static void launch_dec(const Q4kTargets& tg, const Act16& a, float* out, int64_t
     const uint4* fr = (const uint4*)a.frag;
     if (a.rows_pad == 32) {
         if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 2>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps,
-                  early);
+                  early, (const float*)nullptr, (int64_t)0, 0);
         else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 2>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps,
-                  early);
+                  early, (const float*)nullptr, (int64_t)0, 0);
         return;
     }
     if (W == 8) SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 8, 1>), grid, dim3(512), 0, s, tg, fr, out, ldo, ss, nblk, bps,
-                  early);
+                  early, (const float*)nullptr, (int64_t)0, 0);
     else SH_LAUNCH(e0, e1, (q4k_dec_kernel<R, TILED, 4, 1>), grid, dim3(256), 0, s, tg, fr, out, ldo, ss, nblk, bps,
-                  early);
+                  early, (const float*)nullptr, (int64_t)0, 0);
 }
 
 constexpr int PF_R = 2, PF_WAVES = 8;
@@ -921,6 +970,50 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         if (R == 4) launch_dec<4, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
         else if (R == 2) launch_dec<2, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
         else launch_dec<1, false>(tg, a, out, ldo, split_stride, nblk, bps, S, s, ev_start, ev_stop);
+    }
+    SH_CHECK_LAUNCH();
+    *S_out = S;
+    return 0;
+}
+
+// The C ABI's Q4_K matmul of 1 < rows <= 16 f32 rows in one launch (plus the
+// split sum): the decode kernel in its CONV form, on the decode plan.
+template <int R, bool TILED>
+static void launch_dec_conv(const Q4kTargets& tg, const float* X, int64_t ldx, int rows, float* out, int64_t ldo,
+                            int64_t ss, int nblk, int bps, int nsplit, hipStream_t s) {
+    const dim3 grid((tg.grp_end + 7) / 8, nsplit);
+    hipLaunchKernelGGL((q4k_dec_kernel<R, TILED, 8, 1, true>), grid, dim3(512), 0, s, tg, (const uint4*)nullptr,
+                       out, ldo, ss, nblk, bps, 0, X, ldx, rows);
+}
+
+int launch_q4k_conv(const Q4kTarget& t, bool tiled, const float* X, int64_t ldx, int rows, int K, float* out,
+                    int64_t ldo, int64_t split_stride, int max_splits, int* S_out, hipStream_t s) {
+    const int nblk = K / QK;
+    if (rows < 1 || rows > 16 || nblk < 1 || K % QK || t.M < 1) {
+        set_error(-1, "q4k: %d rows of K=%d for the one-tile kernel", rows, K);
+        return -1;
+    }
+    if (dec_waves() != 8) return 1;                   // the caller stages the operand instead
+    int tiles = (t.M + 15) / 16;
+    int R, S;
+    dec_plan(&tiles, 1, nblk, max_splits, &R, &S);
+    const int bps = (nblk + S - 1) / S;
+    S = (nblk + bps - 1) / bps;
+    Q4kTargets tg{};
+    tg.w[0] = (const uint8_t*)t.w;
+    tg.M[0] = t.M;
+    tg.col[0] = (int)t.col;
+    tg.grp0[0] = 0;
+    tg.n = 1;
+    tg.grp_end = (tiles + R - 1) / R;
+    if (tiled) {
+        if (R == 4) launch_dec_conv<4, true>(tg, X, ldx, rows, out, ldo, split_stride, nblk, bps, S, s);
+        else if (R == 2) launch_dec_conv<2, true>(tg, X, ldx, rows, out, ldo, split_stride, nblk, bps, S, s);
+        else launch_dec_conv<1, true>(tg, X, ldx, rows, out, ldo, split_stride, nblk, bps, S, s);
+    } else {
+        if (R == 4) launch_dec_conv<4, false>(tg, X, ldx, rows, out, ldo, split_stride, nblk, bps, S, s);
+        else if (R == 2) launch_dec_conv<2, false>(tg, X, ldx, rows, out, ldo, split_stride, nblk, bps, S, s);
+        else launch_dec_conv<1, false>(tg, X, ldx, rows, out, ldo, split_stride, nblk, bps, S, s);
     }
     SH_CHECK_LAUNCH();
     *S_out = S;
