@@ -71,9 +71,10 @@ def test_dequant_bitexact_random(hip, orc):
 
 
 @pytest.mark.parametrize("M,K", [(256, 256), (200, 512), (4096, 4096), (1024, 14336)])
-# 70, 90 and 100 rows: the prompt kernel's last group of activation tiles
-# holds one, two and three of its four tiles
-@pytest.mark.parametrize("B", [1, 3, 16, 17, 64, 70, 90, 100])
+# 3, 9 and 16 rows: the one-tile kernel that makes its operand from the f32
+# rows; 70, 90 and 100 rows: the prompt kernel's last group of activation
+# tiles holds one, two and three of its four tiles
+@pytest.mark.parametrize("B", [1, 3, 9, 16, 17, 64, 70, 90, 100])
 def test_matmul_q4k(hip, orc, M, K, B):
     if M * K > 4096 * 4096 and B > 17:
         pytest.skip("oracle time budget")
