@@ -175,7 +175,7 @@ int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int 
 // operand.  The consumer of the matmul that follows multiplies each row by
 // row_inv_rms() (the matmul is linear in each row), so no kernel has to wait
 // for a whole row.  Rows >= rows write zero operand rows.
-template <bool DELTA>
+template <bool DELTA, int NPRE = 8>
 __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x, const float* __restrict__ delta,
                                                            int nsplit, int64_t split_stride,
                                                            const float* __restrict__ w, int rows, int D, Act16 a,
@@ -189,14 +189,14 @@ __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x
     const int e = kb * QK + 4 * lane;
     float4 yv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < rows) {
-        // x, w and the first eight partials are issued together: one
-        // memory round trip before any arithmetic
+        // x, w and the first NPRE partials are issued together: one memory
+        // round trip before any arithmetic (up to NPRE splits)
         float* xr = x + (size_t)r * D + e;
         const float* dp = DELTA ? delta + (size_t)r * D + e : nullptr;
         float4 xv = *(const float4*)xr;
         const float4 wv = *(const float4*)(w + e);
-        Split4 pre;
-        if constexpr (DELTA) pre = split_load4(dp, nsplit, split_stride);
+        Split4N<NPRE> pre;
+        if constexpr (DELTA) pre = split_load4<NPRE>(dp, nsplit, split_stride);
         if constexpr (DELTA) {
             const float4 sm = split_fin4(pre, dp, nsplit, split_stride);
             xv.x += sm.x; xv.y += sm.y; xv.z += sm.z; xv.w += sm.w;
@@ -223,7 +223,10 @@ int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_
     }
     const int nblk = D / QK;
     const dim3 grid((nblk + 3) / 4, a.rows_pad);
-    if (delta && nsplit > 0)
+    if (delta && nsplit > 8)   // the down projection's 14 splits at 16 rows: all in one round trip
+        hipLaunchKernelGGL((residual_act_kernel<true, 16>), grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w,
+                           rows, D, a, ssq);
+    else if (delta && nsplit > 0)
         hipLaunchKernelGGL(residual_act_kernel<true>, grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w, rows,
                            D, a, ssq);
     else

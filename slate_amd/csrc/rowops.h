@@ -38,12 +38,14 @@ __device__ __forceinline__ float split_sum1(const float* p, int n, int64_t strid
 // kernel can issue them together with its other independent loads;
 // split_fin4 / split_fin1 then add them (and any further splits) in the same
 // order and with the same result as split_sum4 / split_sum1.
-struct Split4 { float4 t[8]; };
+template <int N = 8> struct Split4N { float4 t[N]; };
+using Split4 = Split4N<8>;
 struct Split1 { float t[8]; };
-__device__ __forceinline__ Split4 split_load4(const float* p, int n, int64_t stride) {
-    Split4 r;
+template <int N = 8>
+__device__ __forceinline__ Split4N<N> split_load4(const float* p, int n, int64_t stride) {
+    Split4N<N> r;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r.t[i] = *(const float4*)(p + (int64_t)min(i, max(n - 1, 0)) * stride);
+    for (int i = 0; i < N; ++i) r.t[i] = *(const float4*)(p + (int64_t)min(i, max(n - 1, 0)) * stride);
     return r;
 }
 __device__ __forceinline__ Split1 split_load1(const float* p, int n, int64_t stride) {
@@ -52,12 +54,14 @@ __device__ __forceinline__ Split1 split_load1(const float* p, int n, int64_t str
     for (int i = 0; i < 8; ++i) r.t[i] = p[(int64_t)min(i, max(n - 1, 0)) * stride];
     return r;
 }
-__device__ __forceinline__ float4 split_fin4(const Split4& r, const float* p, int n, int64_t stride) {
+// (N = 16 loads sixteen partials up front: one round trip up to 16 splits)
+template <int N = 8>
+__device__ __forceinline__ float4 split_fin4(const Split4N<N>& r, const float* p, int n, int64_t stride) {
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < N; ++i)
         if (i < n) { s.x += r.t[i].x; s.y += r.t[i].y; s.z += r.t[i].z; s.w += r.t[i].w; }
-    for (int k = 8; k < n; k += 8) {
+    for (int k = N; k < n; k += 8) {
         float4 t[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) t[i] = *(const float4*)(p + (int64_t)min(k + i, n - 1) * stride);
