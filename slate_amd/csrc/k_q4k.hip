@@ -780,7 +780,7 @@ static int dec_waves() {
 static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, int* S_out) {
     const int R_env = knobs().q4k_r;
     const int S_env = knobs().q4k_s;
-    const int waves_target = knobs().q4k_wgs * 4;   // 2304 waves by default
+    const int waves_target = knobs().q4k_wgs * 4;   // 1664 waves by default
     if (s_max > nblk / 2) s_max = nblk / 2;
     if (s_max < 1) s_max = 1;
     int R_out_v = (R_env == 1 || R_env == 2 || R_env == 4) ? R_env : 1, S_out_v = s_max;
