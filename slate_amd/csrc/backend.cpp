@@ -125,7 +125,7 @@ Knobs read_knobs() {
     k.q4k_r = env_int("SLATE_HIP_Q4K_R", 0);
     if (k.q4k_r != 1 && k.q4k_r != 2 && k.q4k_r != 4) k.q4k_r = 0;
     k.q4k_s = std::max(0, env_int("SLATE_HIP_Q4K_S", 0));
-    k.q4k_wgs = std::max(1, env_int("SLATE_HIP_Q4K_WGS", 416));
+    k.q4k_wgs = std::max(1, env_int("SLATE_HIP_Q4K_WGS", 384));
     k.q4k_pf_s = std::max(0, env_int("SLATE_HIP_Q4K_PF_S", 0));
     k.q4k_pf_nt = env_int("SLATE_HIP_Q4K_PF_NT", 0);
     k.q4k_dec32 = env_int("SLATE_HIP_Q4K_DEC32", 1) != 0;

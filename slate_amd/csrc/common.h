@@ -67,7 +67,7 @@ struct Knobs {
     int q4k_w = 8;         // SLATE_HIP_Q4K_W: waves per decode workgroup (4 or 8)
     int q4k_r = 0;         // SLATE_HIP_Q4K_R: weight tiles per wave (1, 2, 4; 0 = plan)
     int q4k_s = 0;         // SLATE_HIP_Q4K_S: decode split count (0 = plan)
-    int q4k_wgs = 416;     // SLATE_HIP_Q4K_WGS: decode workgroup target of the plan
+    int q4k_wgs = 384;     // SLATE_HIP_Q4K_WGS: decode workgroup target of the plan
     int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
     int q4k_pf_nt = 0;     // SLATE_HIP_Q4K_PF_NT: 2 or 4 activation tiles per prompt workgroup (0 = plan)
     int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one

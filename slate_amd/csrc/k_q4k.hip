@@ -767,38 +767,54 @@ __global__ __launch_bounds__(64 * WAVES) void q4k_pf_kernel(Q4kTargets tg, const
     else run(std::integral_constant<int, (NT > 3 ? 3 : 1)>{});
 }
 
-// Decode plan: the largest R in {4, 2, 1}, then the fewest splits, that give
-// at least `target` workgroups (about two per CU).  Splits keep >= 2 blocks
-// each: a one-block split never overlaps its weight prefetch with compute.
-// Waves per decode workgroup: 8 by default (measured 2 % faster per decode
-// step than 4, since each staged activation block feeds twice the weight
-// tiles, and 16 was 8 % slower); SLATE_HIP_Q4K_W=4 selects four.
+// Decode plan: the fewest splits, then the larger R of {2, 1}, that give at
+// least `target` workgroups while a split holds at most bps_max blocks (a
+// wave's chain of blocks is latency-bound), or that give twice the target,
+// where the workgroups per CU hide a longer chain.  Fewer splits mean fewer
+// split-K partials for the consumers to read.  Matmuls whose partials feed
+// the engine's consumers (attention prologue, residual and SwiGLU
+// epilogues) allow 8 blocks per split: at the 8B shapes and 16 rows QKV
+// R 1 / S 4, O R 1 / S 8, gate+up R 2 / S 2, down R 1 / S 8 and the LM head
+// R 2 / S 1, each the fastest decode step of the per-shape choices measured
+// (decode step -1.5 to -1.8 % against a largest-R-first rule at the same
+// target).  The C ABI's matmul of 2-16 rows, whose partials only a split
+// sum reads, allows 4 (14336x4096 at 16 rows: 16.9 vs 21.3 us with 8).
+// Splits keep >= 2 blocks each: a one-block split never overlaps its weight
+// prefetch with compute.  Waves per decode workgroup: 8 by default
+// (measured 2 % faster per decode step than 4, since each staged activation
+// block feeds twice the weight tiles, and 16 was 8 % slower);
+// SLATE_HIP_Q4K_W=4 selects four.
+constexpr int DEC_BPS_STEP = 8, DEC_BPS_OP = 4;
+
 static int dec_waves() {
     return knobs().q4k_w;
 }
 
-static void dec_plan(const int* tiles, int n, int nblk, int s_max, int* R_out, int* S_out) {
+static void dec_plan(const int* tiles, int n, int nblk, int s_max, int bps_max, int* R_out, int* S_out) {
     const int R_env = knobs().q4k_r;
     const int S_env = knobs().q4k_s;
-    const int waves_target = knobs().q4k_wgs * 4;   // 1664 waves by default
+    const int W = dec_waves();
+    // SLATE_HIP_Q4K_WGS counts four-wave workgroups: 192 of eight waves by default
+    const int target = std::max(1, knobs().q4k_wgs * 4 / W);
     if (s_max > nblk / 2) s_max = nblk / 2;
     if (s_max < 1) s_max = 1;
-    int R_out_v = (R_env == 1 || R_env == 2 || R_env == 4) ? R_env : 1, S_out_v = s_max;
+    // R = 4 only when asked for: at the same target, two tiles per wave with
+    // half the splits (twice the blocks per wave) measured faster (gate+up
+    // 2x14336x4096 at 16 rows: 18.0 vs 19.8 us; LM head equal)
+    const bool r_fixed = R_env == 1 || R_env == 2 || R_env == 4;
+    int R_out_v = r_fixed ? R_env : 1, S_out_v = s_max;
     bool done = false;
-    // R = 4 only when asked for: at the same wave target, two tiles per wave
-    // with half the splits (twice the blocks per wave) measured faster
-    // (gate+up 2x14336x4096 at 16 rows: 18.0 vs 19.8 us; LM head equal)
-    for (int R = R_env == 4 ? 4 : 2; R >= 1 && !done; R >>= 1) {
-        if ((R_env == 1 || R_env == 2 || R_env == 4) && R != R_env) continue;
-        int groups = 0;
-        for (int i = 0; i < n; ++i) groups += (tiles[i] + R - 1) / R;
-        for (int S = 1; S <= s_max; S *= 2) {
-            const int W = dec_waves();
-            if ((groups + W - 1) / W * S >= waves_target / W) {
+    for (int S = 1; S <= s_max && !done; S *= 2) {
+        const int bps = (nblk + S - 1) / S;
+        for (int R = r_fixed ? R_env : 2; R >= 1 && !done; R >>= 1) {
+            if (r_fixed && R != R_env) continue;
+            int groups = 0;
+            for (int i = 0; i < n; ++i) groups += (tiles[i] + R - 1) / R;
+            const int wgs = (groups + W - 1) / W * S;
+            if (wgs >= target && (bps <= bps_max || wgs >= 2 * target)) {
                 R_out_v = R;
                 S_out_v = S;
                 done = true;
-                break;
             }
         }
     }
@@ -948,7 +964,7 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
     int tiles[3];
     for (int i = 0; i < n; ++i) tiles[i] = (t[i].M + 15) / 16;
     int R, S;
-    dec_plan(tiles, n, nblk, max_splits, &R, &S);
+    dec_plan(tiles, n, nblk, max_splits, DEC_BPS_STEP, &R, &S);
     const int bps = (nblk + S - 1) / S;
     S = (nblk + bps - 1) / bps;                       // every split gets >= 1 block
     Q4kTargets tg{};
@@ -996,7 +1012,7 @@ int launch_q4k_conv(const Q4kTarget& t, bool tiled, const float* X, int64_t ldx,
     if (dec_waves() != 8) return 1;                   // the caller stages the operand instead
     int tiles = (t.M + 15) / 16;
     int R, S;
-    dec_plan(&tiles, 1, nblk, max_splits, &R, &S);
+    dec_plan(&tiles, 1, nblk, max_splits, DEC_BPS_OP, &R, &S);
     const int bps = (nblk + S - 1) / S;
     S = (nblk + bps - 1) / bps;
     Q4kTargets tg{};
