@@ -328,6 +328,7 @@ int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64
 // u = sum_s up[s] (backend_cpu.c:78-97 semantics, expf form), stored as f32
 // (y != nullptr, [rows][H]) and/or as the operand of the down projection.
 // One wave per 256-element block of a row (H % 256 == 0).
+template <int NPRE>
 __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, const float* __restrict__ gate,
                                                        const float* __restrict__ up, int rows, int H, int nsplit,
                                                        int64_t split_stride, int64_t ld, Act16 a, int act,
@@ -342,7 +343,8 @@ __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, co
         const float* gp = gate + (size_t)r * ld + e;
         const float* upp = up + (size_t)r * ld + e;
         // gate, up and the row's block sums of squares in one round trip
-        const Split4 pg = split_load4(gp, nsplit, split_stride), pu = split_load4(upp, nsplit, split_stride);
+        const Split4N<NPRE> pg = split_load4<NPRE>(gp, nsplit, split_stride);
+        const Split4N<NPRE> pu = split_load4<NPRE>(upp, nsplit, split_stride);
         RmsPre rp;
         if (rn.ssq) rp = row_rms_load(rn.ssq, r, rn.nblk);
         float4 g = split_fin4(pg, gp, nsplit, split_stride), u = split_fin4(pu, upp, nsplit, split_stride);
@@ -367,8 +369,14 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
     }
     const int nblk = H / QK;
     dim3 grid((nblk + 3) / 4, a ? a->rows_pad : rows);
-    hipLaunchKernelGGL(silu_act_kernel, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride, ld,
-                       a ? *a : Act16{}, a ? 1 : 0, rn);
+    // unsplit gate+up (prompt steps): registers for one partial each, so
+    // more waves per SIMD on the prompt rows' large grids
+    if (nsplit <= 1)
+        hipLaunchKernelGGL(silu_act_kernel<1>, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride,
+                           ld, a ? *a : Act16{}, a ? 1 : 0, rn);
+    else
+        hipLaunchKernelGGL(silu_act_kernel<8>, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride,
+                           ld, a ? *a : Act16{}, a ? 1 : 0, rn);
     SH_CHECK_LAUNCH();
     return 0;
 }
