@@ -830,15 +830,19 @@ __device__ __forceinline__ float4 merge_chunks(const P& pp, size_t p0, int nch, 
 // One wave per 256 output elements of a token row (lane: 4 consecutive
 // elements of one head); with `act` the row also goes out as the Q4_K
 // activation operand (padding rows t >= T as zeros).
-__global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ po,
-                                                         const float* __restrict__ pml,
-                                                         const int32_t* __restrict__ tok_pos, int T, int Hq,
-                                                         int HD, int nch_max, Act16 a, int act) {
+// TILE (with the operand): a 512-thread workgroup per (block, 8-row half
+// tile), wave w = row w of the half, the operand written by
+// act16_store_tile.
+template <bool TILE>
+__device__ __forceinline__ void attn_merge_body(float* __restrict__ out, const float* __restrict__ po,
+                                                const float* __restrict__ pml, const int32_t* __restrict__ tok_pos,
+                                                int T, int Hq, int HD, int nch_max, const Act16& a, int act,
+                                                uint4* s_t) {
     const int lane = threadIdx.x & 63;
-    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int kb = TILE ? blockIdx.x : blockIdx.x * 4 + (threadIdx.x >> 6);
     const int D = Hq * HD;
-    if (kb * 256 >= D) return;                     // whole wave
-    const int t = blockIdx.y;
+    if (!TILE && kb * 256 >= D) return;           // whole wave
+    const int t = TILE ? blockIdx.y * 8 + (threadIdx.x >> 6) : blockIdx.y;
     const int e = kb * 256 + 4 * lane;
     float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
     if (t < T && e < D) {
@@ -848,7 +852,36 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out
         res = merge_chunks(PartPlain{po, pml}, ((size_t)t * Hq + hq) * nch_max, nch, HD, d);
         *(float4*)(out + (size_t)t * D + e) = res;
     }
-    if (act) act16_store_block(a, t, kb, lane, res);
+    if constexpr (TILE) act16_store_tile<8>(a, blockIdx.y >> 1, blockIdx.y & 1, kb, s_t, res);
+    else if (act) act16_store_block(a, t, kb, lane, res);
+}
+__global__ __launch_bounds__(256) void attn_merge_kernel(float* __restrict__ out, const float* __restrict__ po,
+                                                         const float* __restrict__ pml,
+                                                         const int32_t* __restrict__ tok_pos, int T, int Hq,
+                                                         int HD, int nch_max, Act16 a, int act) {
+    attn_merge_body<false>(out, po, pml, tok_pos, T, Hq, HD, nch_max, a, act, nullptr);
+}
+__global__ __launch_bounds__(512) void attn_merge_tile_kernel(float* __restrict__ out, const float* __restrict__ po,
+                                                               const float* __restrict__ pml,
+                                                               const int32_t* __restrict__ tok_pos, int T, int Hq,
+                                                               int HD, int nch_max, Act16 a) {
+    __shared__ uint4 s_t[ACT_FRAG_UNITS];
+    attn_merge_body<true>(out, po, pml, tok_pos, T, Hq, HD, nch_max, a, 1, s_t);
+}
+
+// The chunk merge of T query rows into out (and the operand: by 8-row half
+// tiles when there is more than one tile).
+static void launch_merge(float* out, const float* po, const float* pml, const int32_t* tok_pos, int T, int Hq,
+                         int HD, int nch_max, const Act16* act, hipStream_t s, hipEvent_t ev_stop) {
+    const int nb = (Hq * HD + 255) / 256;
+    if (act && act->rows_pad > 16 && (Hq * HD) % 256 == 0) {
+        SH_LAUNCH(nullptr, ev_stop, attn_merge_tile_kernel, dim3(nb, act->rows_pad / 8), dim3(512), 0, s, out, po,
+                  pml, tok_pos, T, Hq, HD, nch_max, *act);
+        return;
+    }
+    dim3 mgrid((nb + 3) / 4, act ? act->rows_pad : T);
+    SH_LAUNCH(nullptr, ev_stop, attn_merge_kernel, mgrid, dim3(256), 0, s, out, po, pml, tok_pos, T, Hq, HD, nch_max,
+              act ? *act : Act16{}, act ? 1 : 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1233,10 +1266,7 @@ int launch_attention_blocks(float* out, const float* q, const void* Kp, const vo
         SH_CHECK_LAUNCH();
         a.ev0 = nullptr;                           // only the first kernel records the start
     }
-    const int nb = (Hq * HD + 255) / 256;
-    dim3 mgrid((nb + 3) / 4, act ? act->rows_pad : T);
-    SH_LAUNCH(nullptr, ev_stop, attn_merge_kernel, mgrid, dim3(256), 0, s, out, po, pml, tok_pos, T, Hq, HD, nch_max,
-              act ? *act : Act16{}, act ? 1 : 0);
+    launch_merge(out, po, pml, tok_pos, T, Hq, HD, nch_max, act, s, ev_stop);
     SH_CHECK_LAUNCH();
     return 0;
 }
@@ -1387,10 +1417,7 @@ int launch_attention_rope(float* out, void* Kp, void* Vp, const float* part, int
                                                    nch_max, po, pml, pairs, fr);
     if (rc) return rc;
     SH_CHECK_LAUNCH();
-    const int nb = (Hq * HD + 255) / 256;
-    dim3 mgrid((nb + 3) / 4, act ? act->rows_pad : T);
-    SH_LAUNCH(nullptr, ev_stop, attn_merge_kernel, mgrid, dim3(256), 0, s, out, po, pml, tok_pos, T, Hq, HD, nch_max,
-              act ? *act : Act16{}, act ? 1 : 0);
+    launch_merge(out, po, pml, tok_pos, T, Hq, HD, nch_max, act, s, ev_stop);
     SH_CHECK_LAUNCH();
     return 0;
 }

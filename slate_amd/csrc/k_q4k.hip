@@ -79,11 +79,25 @@ __global__ __launch_bounds__(256) void act16_kernel(Act16 a, const float* __rest
     act16_store_block(a, r, kb, lane, v);
 }
 
+// The same conversion by 8-row half tiles (act16_store_tile): a workgroup
+// per (block, half tile), wave w = row w of the half.
+__global__ __launch_bounds__(512) void act16_tile_kernel(Act16 a, const float* __restrict__ X, int64_t ldx) {
+    __shared__ uint4 s_t[ACT_FRAG_UNITS];
+    const int kb = blockIdx.x;
+    const int r = blockIdx.y * 8 + (threadIdx.x >> 6);
+    const float4 v = r < a.rows ? *(const float4*)(X + (size_t)r * ldx + (size_t)kb * QK + 4 * (threadIdx.x & 63))
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+    act16_store_tile<8>(a, blockIdx.y >> 1, blockIdx.y & 1, kb, s_t, v);
+}
+
 int launch_act16_from_f32(const Act16& a, const float* X, int64_t ldx, hipStream_t s) {
     const int nblk = a.K / QK;
     if (nblk <= 0 || a.rows_pad <= 0) return 0;
     if (!a.frag || a.rows_pad % 16) { set_error(-1, "act16: bad operand buffer"); return -1; }
-    hipLaunchKernelGGL(act16_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, a, X, ldx);
+    if (a.rows_pad > 16)
+        hipLaunchKernelGGL(act16_tile_kernel, dim3(nblk, a.rows_pad / 8), dim3(512), 0, s, a, X, ldx);
+    else
+        hipLaunchKernelGGL(act16_kernel, dim3((nblk + 3) / 4, a.rows_pad), dim3(256), 0, s, a, X, ldx);
     SH_CHECK_LAUNCH();
     return 0;
 }

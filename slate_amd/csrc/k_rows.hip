@@ -175,17 +175,20 @@ int launch_rope_rows(float* x, const int32_t* pos, int n_rows, int n_heads, int 
 // operand.  The consumer of the matmul that follows multiplies each row by
 // row_inv_rms() (the matmul is linear in each row), so no kernel has to wait
 // for a whole row.  Rows >= rows write zero operand rows.
-template <bool DELTA, int NPRE = 8>
-__global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x, const float* __restrict__ delta,
-                                                           int nsplit, int64_t split_stride,
-                                                           const float* __restrict__ w, int rows, int D, Act16 a,
-                                                           float* __restrict__ ssq) {
+// TILE: a 512-thread workgroup per (block, 8-row half tile), wave w = row w
+// of the half, the operand written by act16_store_tile (rows of prompt
+// steps).
+template <bool DELTA, int NPRE, bool TILE>
+__device__ __forceinline__ void residual_act_body(float* __restrict__ x, const float* __restrict__ delta,
+                                                  int nsplit, int64_t split_stride, const float* __restrict__ w,
+                                                  int rows, int D, const Act16& a, float* __restrict__ ssq,
+                                                  uint4* s_t) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int kb = TILE ? blockIdx.x : blockIdx.x * 4 + (threadIdx.x >> 6);
     const int nblk = D / QK;
-    if (kb >= nblk) return;                       // whole wave
-    const int r = blockIdx.y;
+    if (!TILE && kb >= nblk) return;              // whole wave
+    const int r = TILE ? blockIdx.y * 8 + (threadIdx.x >> 6) : blockIdx.y;
     const int e = kb * QK + 4 * lane;
     float4 yv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < rows) {
@@ -211,7 +214,23 @@ __global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x
         if constexpr (DELTA) *(float4*)xr = xv;
         if (lane == 0) ssq[(size_t)r * nblk + kb] = sq;
     }
-    act16_store_block(a, r, kb, lane, yv);
+    if constexpr (TILE) act16_store_tile<8>(a, blockIdx.y >> 1, blockIdx.y & 1, kb, s_t, yv);
+    else act16_store_block(a, r, kb, lane, yv);
+}
+template <bool DELTA, int NPRE = 8>
+__global__ __launch_bounds__(256) void residual_act_kernel(float* __restrict__ x, const float* __restrict__ delta,
+                                                           int nsplit, int64_t split_stride,
+                                                           const float* __restrict__ w, int rows, int D, Act16 a,
+                                                           float* __restrict__ ssq) {
+    residual_act_body<DELTA, NPRE, false>(x, delta, nsplit, split_stride, w, rows, D, a, ssq, nullptr);
+}
+template <bool DELTA, int NPRE = 8>
+__global__ __launch_bounds__(512) void residual_act_tile_kernel(float* __restrict__ x,
+                                                                 const float* __restrict__ delta, int nsplit,
+                                                                 int64_t split_stride, const float* __restrict__ w,
+                                                                 int rows, int D, Act16 a, float* __restrict__ ssq) {
+    __shared__ uint4 s_t[ACT_FRAG_UNITS];
+    residual_act_body<DELTA, NPRE, true>(x, delta, nsplit, split_stride, w, rows, D, a, ssq, s_t);
 }
 
 int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_stride, const float* w, int rows,
@@ -223,7 +242,18 @@ int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_
     }
     const int nblk = D / QK;
     const dim3 grid((nblk + 3) / 4, a.rows_pad);
-    if (delta && nsplit > 8)   // the down projection's 14 splits at 16 rows: all in one round trip
+    if (a.rows_pad > 16) {   // prompt steps: the operand by 8-row half tiles
+        const dim3 tg(nblk, a.rows_pad / 8);
+        if (delta && nsplit > 8)
+            hipLaunchKernelGGL((residual_act_tile_kernel<true, 16>), tg, dim3(512), 0, s, x, delta, nsplit,
+                               split_stride, w, rows, D, a, ssq);
+        else if (delta && nsplit > 0)
+            hipLaunchKernelGGL((residual_act_tile_kernel<true>), tg, dim3(512), 0, s, x, delta, nsplit, split_stride,
+                               w, rows, D, a, ssq);
+        else
+            hipLaunchKernelGGL((residual_act_tile_kernel<false>), tg, dim3(512), 0, s, x, delta, nsplit,
+                               split_stride, w, rows, D, a, ssq);
+    } else if (delta && nsplit > 8)   // the down projection's 14 splits at 16 rows: all in one round trip
         hipLaunchKernelGGL((residual_act_kernel<true, 16>), grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w,
                            rows, D, a, ssq);
     else if (delta && nsplit > 0)
@@ -328,15 +358,19 @@ int launch_rmsnorm_act(float* y, float* x, const float* delta, int nsplit, int64
 // u = sum_s up[s] (backend_cpu.c:78-97 semantics, expf form), stored as f32
 // (y != nullptr, [rows][H]) and/or as the operand of the down projection.
 // One wave per 256-element block of a row (H % 256 == 0).
-template <int NPRE>
-__global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, const float* __restrict__ gate,
-                                                       const float* __restrict__ up, int rows, int H, int nsplit,
-                                                       int64_t split_stride, int64_t ld, Act16 a, int act,
-                                                       RowNorm rn) {
+// TILE (with the operand): a 512-thread workgroup per (block, 8-row half
+// tile), wave w = row w of the half, the operand written by
+// act16_store_tile (half tiles: at 114 VGPRs two such workgroups share a
+// CU, where one 16-row workgroup would hold it alone).
+template <int NPRE, bool TILE>
+__device__ __forceinline__ void silu_act_body(float* __restrict__ y, const float* __restrict__ gate,
+                                              const float* __restrict__ up, int rows, int H, int nsplit,
+                                              int64_t split_stride, int64_t ld, const Act16& a, int act,
+                                              const RowNorm& rn, uint4* s_t) {
     const int lane = threadIdx.x & 63;
-    const int kb = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (kb * QK >= H) return;                     // whole wave
-    const int r = blockIdx.y;
+    const int kb = TILE ? blockIdx.x : blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (!TILE && kb * QK >= H) return;            // whole wave
+    const int r = TILE ? blockIdx.y * 8 + (threadIdx.x >> 6) : blockIdx.y;
     const int e = kb * QK + 4 * lane;
     float4 h = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < rows) {
@@ -357,7 +391,22 @@ __global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, co
                         (g.z / (1.0f + expf(-g.z))) * u.z, (g.w / (1.0f + expf(-g.w))) * u.w);
         if (y) *(float4*)(y + (size_t)r * H + e) = h;
     }
-    if (act) act16_store_block(a, r, kb, lane, h);
+    if constexpr (TILE) act16_store_tile<8>(a, blockIdx.y >> 1, blockIdx.y & 1, kb, s_t, h);
+    else if (act) act16_store_block(a, r, kb, lane, h);
+}
+template <int NPRE>
+__global__ __launch_bounds__(256) void silu_act_kernel(float* __restrict__ y, const float* __restrict__ gate,
+                                                       const float* __restrict__ up, int rows, int H, int nsplit,
+                                                       int64_t split_stride, int64_t ld, Act16 a, int act,
+                                                       RowNorm rn) {
+    silu_act_body<NPRE, false>(y, gate, up, rows, H, nsplit, split_stride, ld, a, act, rn, nullptr);
+}
+__global__ __launch_bounds__(512) void silu_act_tile_kernel(float* __restrict__ y, const float* __restrict__ gate,
+                                                             const float* __restrict__ up, int rows, int H,
+                                                             int nsplit, int64_t split_stride, int64_t ld, Act16 a,
+                                                             RowNorm rn) {
+    __shared__ uint4 s_t[ACT_FRAG_UNITS];
+    silu_act_body<1, true>(y, gate, up, rows, H, nsplit, split_stride, ld, a, 1, rn, s_t);
 }
 
 int launch_silu_act(float* y, const float* gate, const float* up, int rows, int H, int nsplit,
@@ -370,8 +419,12 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
     const int nblk = H / QK;
     dim3 grid((nblk + 3) / 4, a ? a->rows_pad : rows);
     // unsplit gate+up (prompt steps): registers for one partial each, so
-    // more waves per SIMD on the prompt rows' large grids
-    if (nsplit <= 1)
+    // more waves per SIMD on the prompt rows' large grids; with the operand,
+    // written by 8-row half tiles
+    if (nsplit <= 1 && a && a->rows_pad > 16)
+        hipLaunchKernelGGL(silu_act_tile_kernel, dim3(nblk, a->rows_pad / 8), dim3(512), 0, s, y, gate, up, rows,
+                           H, nsplit, split_stride, ld, *a, rn);
+    else if (nsplit <= 1)
         hipLaunchKernelGGL(silu_act_kernel<1>, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride,
                            ld, a ? *a : Act16{}, a ? 1 : 0, rn);
     else
