@@ -434,11 +434,12 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
     return 0;
 }
 
-// QKV epilogue, one wave per (token, head): sums the split-K partials of the
-// head's columns, rotates q / k at the token's position (same table and
-// expressions as rope_apply) and writes q to qout, k and v into the KV pool.
+// QKV epilogue, one wave per (token, head), four heads of a token per
+// workgroup: sums the split-K partials of the head's columns, rotates q / k
+// at the token's position (same table and expressions as rope_apply) and
+// writes q to qout, k and v into the KV pool.
 template <typename KVT>
-__global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, KVT* __restrict__ Kpool,
+__global__ __launch_bounds__(256) void rope_kv_kernel(float* __restrict__ qout, KVT* __restrict__ Kpool,
                                                      KVT* __restrict__ Vpool, const float* __restrict__ part,
                                                      int nsplit, int64_t split_stride, int qkv_ld,
                                                      const int32_t* __restrict__ tok2seq,
@@ -447,7 +448,8 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ qout, K
                                                      int n_kv_heads, int hd, int64_t head_stride,
                                                      const float* __restrict__ cs, RowNorm rn) {
 #pragma clang fp contract(off)
-    const int u = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6), t = blockIdx.y, lane = threadIdx.x & 63;
+    if (u >= n_heads + n_kv_heads) return;        // whole wave; no barriers below
     const int D = n_heads * hd, kvd = n_kv_heads * hd, half = hd / 2;
     const int p = tok_pos[t];
     const int ap = p < 0 ? -p : p;
@@ -503,11 +505,11 @@ int launch_rope_kv(float* qout, void* Kpool, void* Vpool, const float* part, int
                    bool kv_f16, hipStream_t s) {
     if (T <= 0) return 0;
     if (kv_f16)
-        hipLaunchKernelGGL(rope_kv_kernel<_Float16>, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout,
+        hipLaunchKernelGGL(rope_kv_kernel<_Float16>, dim3((n_heads + n_kv_heads + 3) / 4, T), dim3(256), 0, s, qout,
                            (_Float16*)Kpool, (_Float16*)Vpool, part, nsplit, split_stride, qkv_ld, tok2seq, tok_pos,
                            kv_base, n_heads, n_kv_heads, hd, head_stride, cs, rn);
     else
-        hipLaunchKernelGGL(rope_kv_kernel<float>, dim3(n_heads + n_kv_heads, T), dim3(64), 0, s, qout,
+        hipLaunchKernelGGL(rope_kv_kernel<float>, dim3((n_heads + n_kv_heads + 3) / 4, T), dim3(256), 0, s, qout,
                            (float*)Kpool, (float*)Vpool, part, nsplit, split_stride, qkv_ld, tok2seq, tok_pos,
                            kv_base, n_heads, n_kv_heads, hd, head_stride, cs, rn);
     SH_CHECK_LAUNCH();
