@@ -943,16 +943,17 @@ int launch_q4k(const Q4kTarget* t, int n, bool tiled, const Act16& a, float* out
         // four activation tiles per workgroup (one workgroup per CU: its two
         // operand buffers take 147 KiB of LDS), or two (two per CU) when the
         // four-tile plan runs two or more rounds of workgroups and leaves the
-        // last under 60 % full: half-size workgroups fill that round better
+        // last one partly filled: half-size workgroups fill that round better
         // (gate+up 2x14336x4096 at 320 rows 184 vs 202 us, 512 rows 269 vs
-        // 280 us; 70B gate+up at 384 rows 799 vs 810 us) and are 1-7 % slower
-        // where the rounds come out even or one round holds everything (every
-        // other 8B and 70B shape measured at 96-1024 rows)
+        // 280 us; 70B gate+up at 384 rows 799 vs 810 us), and over a whole
+        // bench window this threshold beat 60 / 75 / 85 % fill (mixed steps
+        // -1.5 % against 60 %, the 70B serving steps unchanged); where the
+        // rounds come out even or one round holds everything, four tiles
         double fill = 1.0;
         int rounds = 1;
         int NT = act_tiles >= 4 ? 4 : 2;
         int S = plan(NT, &fill, &rounds);
-        if (NT == 4 && rounds >= 2 && fill < 0.6) {
+        if (NT == 4 && rounds >= 2 && fill < 1.0) {
             NT = 2;
             S = plan(2, &fill, &rounds);
         }
