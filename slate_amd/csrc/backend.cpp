@@ -129,7 +129,7 @@ Knobs read_knobs() {
     k.q4k_pf_s = std::max(0, env_int("SLATE_HIP_Q4K_PF_S", 0));
     k.q4k_pf_nt = env_int("SLATE_HIP_Q4K_PF_NT", 0);
     k.q4k_dec32 = env_int("SLATE_HIP_Q4K_DEC32", 1) != 0;
-    k.q4k_early = env_int("SLATE_HIP_Q4K_EARLY", 1) != 0;
+    k.q4k_early = env_int("SLATE_HIP_Q4K_EARLY", 0) != 0;
     k.gemv1 = env_int("SLATE_HIP_GEMV1", 1) != 0;
     k.row_pad64 = env_int("SLATE_HIP_ROW_PAD64", 0) != 0;
     k.q8_r = env_int("SLATE_HIP_Q8_R", 0);

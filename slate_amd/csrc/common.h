@@ -71,7 +71,7 @@ struct Knobs {
     int q4k_pf_s = 0;      // SLATE_HIP_Q4K_PF_S: prompt-kernel split count (0 = plan)
     int q4k_pf_nt = 0;     // SLATE_HIP_Q4K_PF_NT: 2 or 4 activation tiles per prompt workgroup (0 = plan)
     int q4k_dec32 = 1;     // SLATE_HIP_Q4K_DEC32=0: 17..32 rows on the prompt kernel, not the decode one
-    int q4k_early = 1;     // SLATE_HIP_Q4K_EARLY=0: the decode kernel issues block 1 only after block 0 landed
+    int q4k_early = 0;     // SLATE_HIP_Q4K_EARLY=1: the decode kernel issues block 1 together with block 0
     int gemv1 = 1;         // SLATE_HIP_GEMV1=0: one-row C-ABI matvecs of tiled weights on the vector-ALU GEMV
     int row_pad64 = 0;     // SLATE_HIP_ROW_PAD64=1: rows beyond 64 padded to multiples of 64, not 16
     int q8_r = 0;          // SLATE_HIP_Q8_R, _S, _WGS: the same for the Q8_0 matmul

@@ -713,7 +713,7 @@ SWITCHES = [("SLATE_HIP_FUSED_NORM", "0", "q4k"), ("SLATE_HIP_ATTN_MFMA", "0", "
             ("SLATE_HIP_Q4K_R", "1", "q4k"), ("SLATE_HIP_Q4K_R", "4", "q4k"), ("SLATE_HIP_Q4K_W", "4", "q4k"),
             ("SLATE_HIP_Q4K_S", "1", "q4k"), ("SLATE_HIP_Q4K_S", "3", "q4k"), ("SLATE_HIP_Q4K_WGS", "64", "q4k"),
             ("SLATE_HIP_Q4K_PF_S", "3", "q4k"), ("SLATE_HIP_Q4K_PF_NT", "2", "q4k"),
-            ("SLATE_HIP_Q4K_PF_NT", "4", "q4k"), ("SLATE_HIP_Q4K_DEC32", "0", "q4k"),
+            ("SLATE_HIP_Q4K_PF_NT", "4", "q4k"), ("SLATE_HIP_Q4K_DEC32", "0", "q4k"), ("SLATE_HIP_Q4K_EARLY", "1", "q4k"),
             ("SLATE_HIP_Q8_R", "1", "q8_0"), ("SLATE_HIP_Q8_R", "4", "q8_0"),
             ("SLATE_HIP_Q8_S", "2", "q8_0"), ("SLATE_HIP_Q8_WGS", "64", "q8_0")]
 
