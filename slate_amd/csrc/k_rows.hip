@@ -185,7 +185,7 @@ __device__ __forceinline__ void residual_act_body(float* __restrict__ x, const f
                                                   uint4* s_t) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    const int kb = TILE ? blockIdx.x : blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int kb = TILE ? blockIdx.x : blockIdx.x * (int)(blockDim.x >> 6) + (threadIdx.x >> 6);
     const int nblk = D / QK;
     if (!TILE && kb >= nblk) return;              // whole wave
     const int r = TILE ? blockIdx.y * 8 + (threadIdx.x >> 6) : blockIdx.y;
@@ -241,7 +241,10 @@ int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_
         return -1;
     }
     const int nblk = D / QK;
-    const dim3 grid((nblk + 3) / 4, a.rows_pad);
+    // row-wise (decode rows): a workgroup per (block, row), so the few rows
+    // of a decode step spread over every CU (at 16 rows four-wave
+    // workgroups used a quarter of them: decode step -0.9 %)
+    const dim3 grid(nblk, a.rows_pad);
     if (a.rows_pad > 16) {   // prompt steps: the operand by 8-row half tiles
         const dim3 tg(nblk, a.rows_pad / 8);
         if (delta && nsplit > 8)
@@ -254,13 +257,13 @@ int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_
             hipLaunchKernelGGL((residual_act_tile_kernel<false>), tg, dim3(512), 0, s, x, delta, nsplit,
                                split_stride, w, rows, D, a, ssq);
     } else if (delta && nsplit > 8)   // the down projection's 14 splits at 16 rows: all in one round trip
-        hipLaunchKernelGGL((residual_act_kernel<true, 16>), grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w,
+        hipLaunchKernelGGL((residual_act_kernel<true, 16>), grid, dim3(64), 0, s, x, delta, nsplit, split_stride, w,
                            rows, D, a, ssq);
     else if (delta && nsplit > 0)
-        hipLaunchKernelGGL(residual_act_kernel<true>, grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w, rows,
+        hipLaunchKernelGGL(residual_act_kernel<true>, grid, dim3(64), 0, s, x, delta, nsplit, split_stride, w, rows,
                            D, a, ssq);
     else
-        hipLaunchKernelGGL(residual_act_kernel<false>, grid, dim3(256), 0, s, x, delta, nsplit, split_stride, w,
+        hipLaunchKernelGGL(residual_act_kernel<false>, grid, dim3(64), 0, s, x, delta, nsplit, split_stride, w,
                            rows, D, a, ssq);
     SH_CHECK_LAUNCH();
     return 0;
@@ -368,7 +371,7 @@ __device__ __forceinline__ void silu_act_body(float* __restrict__ y, const float
                                               int64_t split_stride, int64_t ld, const Act16& a, int act,
                                               const RowNorm& rn, uint4* s_t) {
     const int lane = threadIdx.x & 63;
-    const int kb = TILE ? blockIdx.x : blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int kb = TILE ? blockIdx.x : blockIdx.x * (int)(blockDim.x >> 6) + (threadIdx.x >> 6);
     if (!TILE && kb * QK >= H) return;            // whole wave
     const int r = TILE ? blockIdx.y * 8 + (threadIdx.x >> 6) : blockIdx.y;
     const int e = kb * QK + 4 * lane;
@@ -417,7 +420,9 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
         return -1;
     }
     const int nblk = H / QK;
-    dim3 grid((nblk + 3) / 4, a ? a->rows_pad : rows);
+    // row-wise: a workgroup per (block, row), as the residual epilogue
+    // (decode step -0.6 % against four-wave workgroups)
+    const dim3 grid(nblk, a ? a->rows_pad : rows);
     // unsplit gate+up (prompt steps): registers for one partial each, so
     // more waves per SIMD on the prompt rows' large grids; with the operand,
     // written by 8-row half tiles
@@ -425,10 +430,10 @@ int launch_silu_act(float* y, const float* gate, const float* up, int rows, int 
         hipLaunchKernelGGL(silu_act_tile_kernel, dim3(nblk, a->rows_pad / 8), dim3(512), 0, s, y, gate, up, rows,
                            H, nsplit, split_stride, ld, *a, rn);
     else if (nsplit <= 1)
-        hipLaunchKernelGGL(silu_act_kernel<1>, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride,
+        hipLaunchKernelGGL(silu_act_kernel<1>, grid, dim3(64), 0, s, y, gate, up, rows, H, nsplit, split_stride,
                            ld, a ? *a : Act16{}, a ? 1 : 0, rn);
     else
-        hipLaunchKernelGGL(silu_act_kernel<8>, grid, dim3(256), 0, s, y, gate, up, rows, H, nsplit, split_stride,
+        hipLaunchKernelGGL(silu_act_kernel<8>, grid, dim3(64), 0, s, y, gate, up, rows, H, nsplit, split_stride,
                            ld, a ? *a : Act16{}, a ? 1 : 0, rn);
     SH_CHECK_LAUNCH();
     return 0;
