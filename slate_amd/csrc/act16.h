@@ -83,8 +83,9 @@ __device__ __forceinline__ void act16_store_block(const Act16& a, int r, int kb,
 // 0-7 of the sum units; the rows' 1/s floats).  Eight rows' units of a group
 // are one whole 128-byte line.  Rows written piece by piece from different
 // workgroups fill each line in 16-byte parts at different times; lines
-// written whole convert 304 x 14336 rows in 8.5 instead of 17.4 us, with the
-// same bytes.  Every thread of the workgroup calls it (it holds a barrier).
+// written whole convert 304 x 14336 rows in 6.8 us (8-row halves) or 8.5 us
+// (16-row tiles) instead of 17.4 us, with the same bytes.  Every thread of
+// the workgroup calls it (it holds a barrier).
 template <int ROWS>
 __device__ __forceinline__ void act16_store_tile(const Act16& a, int tile, int part, int kb, uint4* s, float4 v) {
     static_assert(ROWS == 8 || ROWS == 16, "whole or half tiles");

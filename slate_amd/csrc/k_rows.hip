@@ -256,7 +256,7 @@ int launch_residual_act(float* x, const float* delta, int nsplit, int64_t split_
         else
             hipLaunchKernelGGL((residual_act_tile_kernel<false>), tg, dim3(512), 0, s, x, delta, nsplit,
                                split_stride, w, rows, D, a, ssq);
-    } else if (delta && nsplit > 8)   // the down projection's 14 splits at 16 rows: all in one round trip
+    } else if (delta && nsplit > 8)   // more than eight splits (forced plans): all in one round trip
         hipLaunchKernelGGL((residual_act_kernel<true, 16>), grid, dim3(64), 0, s, x, delta, nsplit, split_stride, w,
                            rows, D, a, ssq);
     else if (delta && nsplit > 0)
